@@ -1,0 +1,140 @@
+/*
+ * laguna_hip.h -- C ABI of liblaguna_hip.so: MI355X (gfx950) kernels for lagunaLab's quantized
+ * KV-cache decode path.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (LQ_OK == 0) and never throws. On failure
+ *    lq_last_error() returns a thread-local message. Arguments are validated before any launch.
+ *  - Pointers are device pointers unless the comment says "host". The library allocates no
+ *    memory; scratch space is passed in as `workspace` (size from the matching *_bytes query).
+ *  - Work is enqueued on `stream` (a hipStream_t, passed as void*) and is asynchronous.
+ *  - bf16 values are passed as uint16_t bit patterns.
+ *
+ * Cache layout (the reference's, laguna_mlx/q8_attn.py:8-10; mlx-lm QuantizedKVCache): per layer
+ *   codes  uint8  [B, Hkv, cap, D*bits/8]  8-bit: one byte per element in order (byte-identical to
+ *                                          MLX's uint32 words, low byte first); 4-bit: two per
+ *                                          byte, even element in the low nibble
+ *   scales bf16   [B, Hkv, cap, D/group]
+ *   biases bf16   [B, Hkv, cap, D/group]
+ * Rows [0, n) of the full-capacity buffers are valid.
+ */
+#ifndef LAGUNA_HIP_H
+#define LAGUNA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_OK 0
+#define LQ_EINVAL 1     /* bad argument (shape, size, dtype contract) */
+#define LQ_EHIP 2       /* HIP runtime error (launch, attribute query) */
+#define LQ_EWORKSPACE 3 /* workspace missing or too small */
+
+#define LQ_MAX_SEQS 64  /* sequences per ragged decode call */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int lq_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* lq_last_error(void);
+
+/*
+ * Quantize-on-append. Replaces mx.quantize inside mlx-lm QuantizedKVCache.update_and_fetch as
+ * called from DequantKVCache.update_and_fetch (laguna_mlx/cache.py:89-90): quantizes
+ * src[B, H, L, D] (bf16, contiguous) group-wise and writes rows [offset, offset+L) of the cache
+ * buffers (capacity `cap` rows). bits in {4, 8}; group_size in {32, 64, 128}; D % group_size == 0.
+ */
+int lq_quantize_append(const uint16_t* src, int64_t B, int64_t H, int64_t L, int64_t D,
+                       uint8_t* codes, uint16_t* scales, uint16_t* biases, int64_t cap,
+                       int64_t offset, int bits, int group_size, void* stream);
+
+/*
+ * Dequantize rows [0, n) of a cache to bf16 out[B, H, n, D]. Replaces mx.dequantize on the
+ * unfused path (laguna_mlx/cache.py:99-100).
+ */
+int lq_dequantize(const uint8_t* codes, const uint16_t* scales, const uint16_t* biases,
+                  int64_t B, int64_t H, int64_t cap, int64_t n, int64_t D, int bits,
+                  int group_size, uint16_t* out, void* stream);
+
+/*
+ * Scratch bytes for lq_decode_attn with the same B / Hq / Hkv / lengths. `lens_host` (host, B
+ * entries) may be NULL, then every sequence has length n. Returns a negative value on bad args.
+ */
+int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                  int64_t n, const int32_t* lens_host);
+
+/* kind for lq_decode_attn / lq_decode_workspace_bytes */
+#define LQ_KV_Q8 8    /* 8-bit affine group-64 codes */
+#define LQ_KV_Q4 4    /* 4-bit affine group-64 codes */
+#define LQ_KV_BF16 16 /* plain bf16 K/V [B, Hkv, cap, D]; scale/bias pointers unused */
+
+/*
+ * Fused single-token decode attention. Replaces q8_decode_attention(q, keys, values, n, scale)
+ * (laguna_mlx/q8_attn.py:102-130: the Metal kernel N1 at :17-99 and the block merge at
+ * :126-130) and generalises it to 4-bit and plain-bf16 caches and to ragged batches.
+ *   q    bf16 [B, Hq, 1, D] contiguous, D == 128, Hq % Hkv == 0, Hq / Hkv <= 8
+ *   kc..vb the cache buffers of one layer (layout above; for LQ_KV_BF16, kc and vc are bf16
+ *          [B, Hkv, cap, D])
+ *   n    valid rows when lens_host == NULL; otherwise lens_host[b] (host array, B <= 64,
+ *        1 <= lens <= cap) gives each sequence's length (variable-length split-K with a
+ *        per-sequence log-sum-exp merge)
+ *   out  bf16 [B, Hq, 1, D]
+ * softmax scale `scale` (the reference passes head_dim**-0.5, laguna_mlx/laguna.py:76).
+ */
+int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const uint16_t* ks,
+                   const uint16_t* kb, const void* vc, const uint16_t* vs, const uint16_t* vb,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
+                   const int32_t* lens_host, float scale, uint16_t* out, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/*
+ * Scratch bytes for lq_q8_verify_attn.
+ */
+int64_t lq_verify_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                                  int64_t n);
+
+/*
+ * Fused multi-query causal verify attention over the 8-bit cache. Replaces the unfused verify
+ * forward of the speculative loop (laguna_mlx/dflash.py:195 -> laguna.py:107 with the causal
+ * mask of laguna.py:183-186, over DequantKVCache's dequantized K/V, cache.py:99-100):
+ *   q   bf16 [B, Hq, L, D] contiguous, 1 <= L <= 16, D == 128; the last L of the n valid rows are
+ *       the block's own keys; query row i sees keys 0 .. n-L+i (bottom-right causal).
+ *   out bf16 [B, Hq, L, D]
+ */
+int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uint16_t* ks,
+                      const uint16_t* kb, const uint8_t* vc, const uint16_t* vs,
+                      const uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                      int64_t D, int64_t cap, int64_t n, float scale, uint16_t* out,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Prompt-lookup draft search. Replaces NgramIndex.propose (laguna_mlx/dflash.py:164-167) for a
+ * history held on the device: finds the most recent start s <= T-g-1 with
+ * hist[s:s+g] == hist[T-g:T] and returns up to n following ids (never past T).
+ *   hist int32 [T] (device)
+ *   out  int32 [2 + n] (device): out[0] = count, out[1] = s (-1 if none), out[2..2+count) ids
+ * 1 <= g <= 16, 1 <= n <= 64.
+ */
+int64_t lq_ngram_workspace_bytes(int64_t T);
+int lq_ngram_propose(const int32_t* hist, int64_t T, int g, int n, int32_t* out,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Greedy acceptance of a verified draft block. Replaces the argmax + longest-prefix loop of
+ * generate_lookup (laguna_mlx/dflash.py:195-198):
+ *   logits fp32 [L, V] (row stride V), drafts int32 [m] (device), m <= L - 1
+ *   out int32 [2 + L] (device): out[0] = k (accepted drafts), out[1] = next token pred[k],
+ *       out[2 + i] = argmax of row i (first index on ties)
+ */
+int64_t lq_accept_workspace_bytes(int64_t L, int64_t V);
+int lq_greedy_accept(const float* logits, int64_t L, int64_t V, const int32_t* drafts,
+                     int64_t m, int32_t* out, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAGUNA_HIP_H */

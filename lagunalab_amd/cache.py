@@ -1,0 +1,282 @@
+"""KV caches for the quantized decode path (PyTorch-ROCm host side, HIP kernels underneath).
+
+Drop-in for ``laguna_mlx/cache.py``:
+
+* :class:`QuantizedKVCache` -- the mlx-lm 0.31.3 class ``DequantKVCache`` wraps
+  (``cache.py:83``): full-capacity buffers grown in steps of 256 rows, quantize-on-append of the
+  new rows at ``offset`` (now the HIP kernel ``lq_quantize_append``), views of the first
+  ``offset`` rows returned, ``trim`` only moves ``offset``.
+* :class:`DequantKVCache` -- same constructor, properties and switches as the reference
+  (``cache.py:66-144``): by default multi-token and single-token steps get dequantized bf16 K/V;
+  ``quantized_decode`` hands single-token steps the packed tuples and exposes ``bits`` for that
+  step only; ``fused_decode`` sets ``fused_step`` and ``attend`` runs the fused HIP kernel.
+  Extension (``fused_verify``, default: follows ``fused_decode``): multi-token steps of up to 16
+  rows -- the speculative verify block -- also take a fused kernel (causal, bottom-right).
+* :func:`make_quantized_cache` -- per-layer factory (``cache.py:147-157``).
+* :class:`RotatingKVCache` -- plain bf16 sliding-window cache for sliding layers (mlx-lm's
+  ``RotatingKVCache(max_size=window)``, kept minimal: the last ``max_size`` rows).
+"""
+from __future__ import annotations
+
+import torch
+
+from .quant import dequantize, quantize_into
+
+
+def create_attention_mask(N: int, offset: int = 0, return_array: bool = False,
+                          window_size: int | None = None):
+    """mlx-lm's convention: None for one row, "causal" for several, or a boolean [N, offset+N]
+    mask (True = attend) aligned to the bottom-right."""
+    if window_size is None and N == 1:
+        return None
+    if window_size is None and not return_array:
+        return "causal"
+    q = torch.arange(offset, offset + N)[:, None]
+    k = torch.arange(offset + N)[None, :]
+    m = k <= q
+    if window_size is not None:
+        m &= k > q - window_size
+    return m
+
+
+class QuantizedKVCache:
+    step = 256
+
+    def __init__(self, group_size: int = 64, bits: int = 8):
+        self.group_size, self.bits = group_size, bits
+        self.keys = self.values = None  # (codes, scales, biases), full capacity
+        self.offset = 0
+
+    def _alloc(self, B, H, rows, D, device):
+        return (torch.zeros((B, H, rows, D * self.bits // 8), dtype=torch.uint8, device=device),
+                torch.zeros((B, H, rows, D // self.group_size), dtype=torch.bfloat16, device=device),
+                torch.zeros((B, H, rows, D // self.group_size), dtype=torch.bfloat16, device=device))
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        B, H, L, Dk = keys.shape
+        Dv = values.shape[-1]
+        prev = self.offset
+        if self.keys is None or prev + L > self.keys[0].shape[2]:
+            new_steps = (self.step + L - 1) // self.step * self.step
+            if self.keys is None:
+                self.keys = self._alloc(B, H, new_steps, Dk, keys.device)
+                self.values = self._alloc(B, H, new_steps, Dv, values.device)
+            else:
+                if prev % self.step != 0:
+                    self.keys = tuple(t[:, :, :prev] for t in self.keys)
+                    self.values = tuple(t[:, :, :prev] for t in self.values)
+                self.keys = tuple(torch.cat([t, z], dim=2) for t, z in
+                                  zip(self.keys, self._alloc(B, H, new_steps, Dk, keys.device)))
+                self.values = tuple(torch.cat([t, z], dim=2) for t, z in
+                                    zip(self.values, self._alloc(B, H, new_steps, Dv, values.device)))
+        self.offset += L
+        quantize_into(keys, *self.keys, prev, self.group_size, self.bits)
+        quantize_into(values, *self.values, prev, self.group_size, self.bits)
+        return (tuple(t[:, :, :self.offset] for t in self.keys),
+                tuple(t[:, :, :self.offset] for t in self.values))
+
+    @property
+    def state(self):
+        if self.keys is None:
+            return None, None
+        if self.offset == self.keys[0].shape[2]:
+            return self.keys, self.values
+        return (tuple(t[:, :, :self.offset] for t in self.keys),
+                tuple(t[:, :, :self.offset] for t in self.values))
+
+    def make_mask(self, N, return_array=False, window_size=None):
+        return create_attention_mask(N, offset=self.offset, return_array=return_array,
+                                     window_size=window_size)
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        n = min(self.offset, n)
+        self.offset -= n
+        return n
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def nbytes(self):
+        if self.keys is None:
+            return 0
+        return sum(t.numel() * t.element_size() for t in (*self.keys, *self.values))
+
+
+class DequantKVCache:
+    """Stores K/V quantized and, by default, hands attention dequantized bf16 K/V
+    (``laguna_mlx/cache.py:66-144``). No ``bits`` attribute except on single-token
+    ``quantized_decode`` steps."""
+
+    def __init__(self, group_size=64, bits=8, quantized_decode=False, fused_decode=False,
+                 fused_verify=None):
+        if fused_decode and (bits, group_size) != (8, 64):
+            raise ValueError("fused_decode needs 8-bit, group_size 64")
+        self.q = QuantizedKVCache(group_size=group_size, bits=bits)
+        self.quantized_decode = quantized_decode
+        self.fused_decode = fused_decode
+        self.fused_verify = fused_decode if fused_verify is None else fused_verify
+        self._quantized_step = False
+        self.fused_step = False
+
+    def update_and_fetch(self, keys, values):
+        qk, qv = self.q.update_and_fetch(keys, values)
+        L = keys.shape[2]
+        # Attention checks `fused_step` and then calls attend(); the K/V returned are unused
+        self.fused_step = self.fused_decode and (L == 1 or (self.fused_verify and L <= 16))
+        if self.fused_step:
+            self._quantized_step = False
+            return qk, qv
+        self._quantized_step = self.quantized_decode and L == 1
+        if self._quantized_step:
+            return qk, qv
+        g, b = self.q.group_size, self.q.bits
+        n = self.q.offset
+        return dequantize(*self.q.keys, g, b, n=n), dequantize(*self.q.values, g, b, n=n)
+
+    def attend(self, queries, scale):
+        """Attention straight off the packed cache: the fused decode kernel for one query row,
+        the fused causal verify kernel for a block of up to 16 rows."""
+        from .q8_attn import q8_decode_attention, q8_verify_attention
+
+        if queries.shape[2] == 1:
+            return q8_decode_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
+        return q8_verify_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
+
+    @property
+    def bits(self):
+        if not self._quantized_step:
+            raise AttributeError("bits")  # hasattr(cache, "bits") is False off quantized steps
+        return self.q.bits
+
+    @property
+    def offset(self):
+        return self.q.offset
+
+    @property
+    def kv_bits(self):
+        return self.q.bits
+
+    @property
+    def group_size(self):
+        return self.q.group_size
+
+    def make_mask(self, *args, **kwargs):
+        return self.q.make_mask(*args, **kwargs)
+
+    @property
+    def state(self):
+        return self.q.state
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        return self.q.trim(n)
+
+    def empty(self):
+        return self.q.empty()
+
+    @property
+    def nbytes(self):
+        return self.q.nbytes
+
+
+class KVCache:
+    """Plain bf16 cache (mlx-lm ``KVCache``): grows in 256-row steps, returns ``[:offset]``."""
+
+    step = 256
+
+    def __init__(self):
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys, values):
+        B, H, L, D = keys.shape
+        prev = self.offset
+        if self.keys is None or prev + L > self.keys.shape[2]:
+            new = (self.step + L - 1) // self.step * self.step
+            zk = torch.zeros((B, H, new, D), dtype=keys.dtype, device=keys.device)
+            zv = torch.zeros((B, H, new, values.shape[-1]), dtype=values.dtype, device=values.device)
+            if self.keys is None:
+                self.keys, self.values = zk, zv
+            else:
+                self.keys = torch.cat([self.keys[:, :, :prev], zk], dim=2)
+                self.values = torch.cat([self.values[:, :, :prev], zv], dim=2)
+        self.offset += L
+        self.keys[:, :, prev:self.offset] = keys
+        self.values[:, :, prev:self.offset] = values
+        return self.keys[:, :, :self.offset], self.values[:, :, :self.offset]
+
+    def make_mask(self, N, return_array=False, window_size=None):
+        return create_attention_mask(N, offset=self.offset, return_array=return_array,
+                                     window_size=window_size)
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        n = min(self.offset, n)
+        self.offset -= n
+        return n
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def state(self):
+        return self.keys[:, :, :self.offset], self.values[:, :, :self.offset]
+
+    @property
+    def nbytes(self):
+        return 0 if self.keys is None else self.keys.nbytes + self.values.nbytes
+
+
+class RotatingKVCache:
+    """Sliding-window bf16 cache: keeps the last ``max_size`` rows; ``offset`` is absolute."""
+
+    def __init__(self, max_size):
+        self.max_size = max_size
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys, values):
+        if self.keys is None:
+            self.keys, self.values = keys, values
+        else:
+            self.keys = torch.cat([self.keys[:, :, -(self.max_size - 1):], keys], dim=2)
+            self.values = torch.cat([self.values[:, :, -(self.max_size - 1):], values], dim=2)
+        self.offset += keys.shape[2]
+        return self.keys, self.values
+
+    def make_mask(self, N, return_array=False, window_size=None):
+        stored = 0 if self.keys is None else self.keys.shape[2]
+        return create_attention_mask(N, offset=stored, return_array=True,
+                                     window_size=window_size or self.max_size)
+
+    def is_trimmable(self):
+        return False
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def nbytes(self):
+        return 0 if self.keys is None else self.keys.nbytes + self.values.nbytes
+
+
+def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, fused_decode=False):
+    """Quantized KV storage on full-attention layers; sliding layers keep their window."""
+    a = model.args
+    if a.head_dim % group_size:
+        raise ValueError(f"head_dim {a.head_dim} is not a multiple of group_size {group_size}")
+    return [
+        RotatingKVCache(max_size=a.sliding_window)
+        if lt == "sliding_attention" else DequantKVCache(group_size=group_size, bits=bits,
+                                                         quantized_decode=quantized_decode,
+                                                         fused_decode=fused_decode)
+        for lt in a.layer_types
+    ]

@@ -1,0 +1,136 @@
+// Shared helpers for the gfx950 kernels of liblaguna_hip.so: status/error reporting, bf16 and
+// fp16 bit tricks, wave64 cross-lane reductions, device properties.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/laguna_hip.h"
+
+namespace lq {
+
+// ---------------------------------------------------------------------------------------------
+// host: error reporting
+// ---------------------------------------------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define LQ_CHECK_ARG(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::lq::set_error(__VA_ARGS__);      \
+      return LQ_EINVAL;                  \
+    }                                    \
+  } while (0)
+
+#define LQ_CHECK_HIP(expr)                                                          \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess) {                                                         \
+      ::lq::set_error("%s failed: %s", #expr, hipGetErrorString(e_));               \
+      return LQ_EHIP;                                                               \
+    }                                                                               \
+  } while (0)
+
+// Launch-error check right after a <<<>>> launch.
+#define LQ_CHECK_LAUNCH(name)                                                       \
+  do {                                                                              \
+    hipError_t e_ = hipGetLastError();                                              \
+    if (e_ != hipSuccess) {                                                         \
+      ::lq::set_error("launch of %s failed: %s", name, hipGetErrorString(e_));      \
+      return LQ_EHIP;                                                               \
+    }                                                                               \
+  } while (0)
+
+// Compute units of the current device (cached per device id).
+int device_cu_count();
+
+// ---------------------------------------------------------------------------------------------
+// device: number formats
+// ---------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16, round to nearest even (NaN -> quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Two codes c0 (byte sel0) and c1 (byte sel1) of `w` as the fp16 pair (1024 + c0, 1024 + c1):
+// 0x64XX is the fp16 number 1024 + XX for XX in [0, 255]. One v_perm_b32. `sel` selects the
+// bytes of `w` for result bytes 0 and 2; bytes 1 and 3 come from the constant 0x64646464.
+__device__ __forceinline__ half2_t codes_as_h2(uint32_t w, uint32_t sel) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
+}
+// selectors for codes_as_h2: bytes (0,1) and (2,3) of w
+constexpr uint32_t SEL_B01 = 0x04010400u;
+constexpr uint32_t SEL_B23 = 0x04030402u;
+
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// ---------------------------------------------------------------------------------------------
+// device: wave64 cross-lane helpers
+// ---------------------------------------------------------------------------------------------
+
+// DPP control codes (GCN/CDNA): quad permutes and row (16-lane) rotations.
+constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_ROR4 = 0x124;   // row_ror:4
+constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 4 lanes, result in all 4 lanes.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp<DPP_QUAD_XOR1>(x);
+  x += dpp<DPP_QUAD_XOR2>(x);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_ROW_ROR4>(x));
+  x = fmaxf(x, dpp<DPP_ROW_ROR8>(x));
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_min(float x) {
+  x = fminf(x, dpp<DPP_QUAD_XOR1>(x));
+  x = fminf(x, dpp<DPP_QUAD_XOR2>(x));
+  x = fminf(x, dpp<DPP_ROW_ROR4>(x));
+  x = fminf(x, dpp<DPP_ROW_ROR8>(x));
+  x = fminf(x, __shfl_xor(x, 16, 64));
+  x = fminf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp<DPP_QUAD_XOR1>(x);
+  x += dpp<DPP_QUAD_XOR2>(x);
+  x += dpp<DPP_ROW_ROR4>(x);
+  x += dpp<DPP_ROW_ROR8>(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+}  // namespace lq

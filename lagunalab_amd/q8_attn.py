@@ -1,0 +1,185 @@
+"""Fused attention over the quantized KV cache, on liblaguna_hip.so.
+
+Drop-in for ``laguna_mlx/q8_attn.py``: :func:`q8_decode_attention` keeps the reference signature
+``q8_decode_attention(q, keys, values, n, scale)`` (``q8_attn.py:102``), its argument meaning
+(full-capacity ``(codes, scales, biases)`` tuples of which the first ``n`` rows are valid, output
+``[B, Hq, 1, D]`` in q's dtype) and its error behaviour (``AssertionError`` for a non-decode
+query, a head_dim other than 128, a cache that is not 8-bit, or too many query heads per KV head,
+``q8_attn.py:110-115``). Codes may be given as uint8 ``[..., D]`` or as MLX-style 32-bit words
+``[..., D // 4]`` (int32/uint32; byte-identical on little-endian hosts).
+
+Additions behind the same layout (the north-star extensions): ragged batches with per-sequence
+lengths (:func:`decode_attention` with ``lens``), the multi-query causal verify step
+(:func:`q8_verify_attention`), and 4-bit / plain-bf16 caches (:func:`decode_attention` with
+``kind``).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+BLOCK = 512  # key-block size of the reference kernel (q8_attn.py:14); kept for callers that import it
+
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-(device, stream) scratch buffer, grown on demand. Calls on one stream are ordered,
+    so reuse is safe; different streams get different buffers."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _as_bytes(codes: torch.Tensor) -> torch.Tensor:
+    """Cache codes as a contiguous uint8 tensor [B, H, cap, row_bytes]."""
+    if codes.dtype in (torch.int32, torch.uint32):
+        codes = codes.contiguous().view(torch.uint8)
+    if codes.dtype != torch.uint8:
+        raise ValueError(f"cache codes must be uint8 or 32-bit words, got {codes.dtype}")
+    return codes.contiguous()
+
+
+def _bf16(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{what} must be bfloat16, got {t.dtype}")
+    return t.contiguous()
+
+
+def _kind_of(keys, D: int) -> int:
+    codes = keys[0]
+    row = codes.shape[-1] * (4 if codes.dtype in (torch.int32, torch.uint32) else 1)
+    if codes.dtype == torch.bfloat16:
+        return _lib.LQ_KV_BF16
+    if row == D:
+        return _lib.LQ_KV_Q8
+    if row == D // 2:
+        return _lib.LQ_KV_Q4
+    raise ValueError(f"cache rows of {row} bytes do not match head_dim {D} at 8 or 4 bits")
+
+
+def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale: float = None,
+                     lens=None) -> torch.Tensor:
+    """Single-token attention over a quantized (or plain bf16) KV cache.
+
+    q [B, Hq, 1, 128] bf16. ``keys``/``values``: ``(codes, scales, biases)`` of shape
+    ``[B, Hkv, cap, .]`` (8- or 4-bit, group 64), or a plain bf16 tensor ``[B, Hkv, cap, 128]``.
+    Either ``n`` (every sequence has ``n`` valid rows) or ``lens`` (B lengths; ragged batch).
+    Returns ``[B, Hq, 1, 128]`` bf16.
+    """
+    lib = _lib.load()
+    if not isinstance(keys, (tuple, list)):
+        keys, values = (keys, None, None), (values, None, None)
+    B, Hq, L, D = q.shape
+    if L != 1:
+        raise ValueError("decode_attention takes one query row per sequence")
+    kind = _kind_of(keys, D)
+    kc, ks, kb = keys
+    vc, vs, vb = values
+    dev = _lib.require_device(q, kc, ks, kb, vc, vs, vb)
+    q = _bf16(q, "q")
+    if kind == _lib.LQ_KV_BF16:
+        kc, vc = _bf16(kc, "keys"), _bf16(vc, "values")
+        ks = kb = vs = vb = None
+    else:
+        kc, vc = _as_bytes(kc), _as_bytes(vc)
+        ks, kb, vs, vb = (_bf16(t, "scales/biases") for t in (ks, kb, vs, vb))
+    if kc.dim() != 4:
+        raise ValueError(f"cache codes must be [B, Hkv, cap, .], got {tuple(kc.shape)}")
+    Hkv, cap = kc.shape[1], kc.shape[2]
+    row = {_lib.LQ_KV_Q8: D, _lib.LQ_KV_Q4: D // 2, _lib.LQ_KV_BF16: D}[kind]
+    for t in (kc, vc):
+        if tuple(t.shape) != (B, Hkv, cap, row):
+            raise ValueError(f"cache buffer {tuple(t.shape)} does not match {(B, Hkv, cap, row)}")
+    if kind != _lib.LQ_KV_BF16:
+        for t in (ks, kb, vs, vb):
+            if tuple(t.shape) != (B, Hkv, cap, D // 64):
+                raise ValueError(f"scales/biases {tuple(t.shape)} do not match {(B, Hkv, cap, D // 64)}")
+    if Hkv < 1 or Hq % Hkv:
+        raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} KV heads")
+    lens_arr = None
+    if lens is not None:
+        lens_list = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
+        if len(lens_list) != B:
+            raise ValueError(f"lens has {len(lens_list)} entries for a batch of {B}")
+        lens_arr = _lib.C.cast((_lib.C.c_int32 * B)(*lens_list), _lib.C.c_void_p)
+        n = 0
+    elif n is None:
+        raise ValueError("give n or lens")
+    if scale is None:
+        scale = D ** -0.5
+    ws_bytes = lib.lq_decode_workspace_bytes(kind, B, Hq, Hkv, D, int(n), lens_arr)
+    if ws_bytes < 0:
+        raise ValueError(lib.lq_last_error().decode())
+    ws = _workspace(dev, ws_bytes)
+    out = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=dev)
+    st = lib.lq_decode_attn(kind, q.data_ptr(), kc.data_ptr(), _lib.ptr(ks), _lib.ptr(kb),
+                            vc.data_ptr(), _lib.ptr(vs), _lib.ptr(vb), B, Hq, Hkv, D, cap, int(n),
+                            lens_arr, float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                            _lib.stream_ptr(dev))
+    _lib.check(st, "lq_decode_attn")
+    return out
+
+
+def q8_decode_attention(q, keys, values, n, scale):
+    """q [B, Hq, 1, D]; keys/values: the cache's full-capacity (codes, scales, biases) tuples,
+    of which the first ``n`` rows are valid. Returns [B, Hq, 1, D] in q's dtype
+    (``laguna_mlx/q8_attn.py:102-130``)."""
+    B, Hq, L, D = q.shape
+    if not (L == 1 and D == 128):
+        raise AssertionError("decode only, head_dim 128")
+    codes = keys[0]
+    words = codes.shape[-1] * (1 if codes.dtype == torch.uint8 else 4) // 4
+    if words != D // 4:
+        raise AssertionError("8-bit, group_size 64 only")
+    hkv = codes.shape[1]
+    G = Hq // hkv
+    if G > 8 or Hq % hkv:
+        raise AssertionError(f"{G} q heads per kv head is too many for one workgroup")
+    out = decode_attention(q.to(torch.bfloat16), keys, values, n=int(n), scale=scale)
+    return out.to(q.dtype)
+
+
+def q8_verify_attention(q, keys, values, n, scale):
+    """Multi-query causal attention for a verify block over the 8-bit cache.
+
+    q [B, Hq, L, 128] with 1 <= L <= 16; the block's own L keys are the last L of the first
+    ``n`` cache rows; query row i sees keys 0 .. n-L+i (bottom-right causal, as the reference's
+    verify forward masks it, ``laguna_mlx/laguna.py:183-186``). Returns [B, Hq, L, 128] in q's
+    dtype."""
+    lib = _lib.load()
+    B, Hq, L, D = q.shape
+    if D != 128 or not 1 <= L <= 16:
+        raise ValueError("verify needs head_dim 128 and 1 <= L <= 16")
+    kc, ks, kb = keys
+    vc, vs, vb = values
+    dev = _lib.require_device(q, kc, ks, kb, vc, vs, vb)
+    qb = _bf16(q.to(torch.bfloat16), "q")
+    kc, vc = _as_bytes(kc), _as_bytes(vc)
+    if kc.shape[-1] != D:
+        raise ValueError("verify runs on the 8-bit cache only")
+    ks, kb, vs, vb = (_bf16(t, "scales/biases") for t in (ks, kb, vs, vb))
+    Hkv, cap = kc.shape[1], kc.shape[2]
+    for t in (kc, vc):
+        if tuple(t.shape) != (B, Hkv, cap, D):
+            raise ValueError(f"cache buffer {tuple(t.shape)} does not match {(B, Hkv, cap, D)}")
+    for t in (ks, kb, vs, vb):
+        if tuple(t.shape) != (B, Hkv, cap, D // 64):
+            raise ValueError(f"scales/biases {tuple(t.shape)} do not match {(B, Hkv, cap, D // 64)}")
+    if not L <= int(n) <= cap:
+        raise ValueError(f"n={n} must cover the {L} block rows and fit the capacity {cap}")
+    ws_bytes = lib.lq_verify_workspace_bytes(B, Hq, Hkv, L, D, int(n))
+    if ws_bytes < 0:
+        raise ValueError(lib.lq_last_error().decode())
+    ws = _workspace(dev, ws_bytes)
+    out = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=dev)
+    st = lib.lq_q8_verify_attn(qb.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                               vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, L, D, cap,
+                               int(n), float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                               _lib.stream_ptr(dev))
+    _lib.check(st, "lq_q8_verify_attn")
+    return out.to(q.dtype)

@@ -1,0 +1,85 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/laguna_hip.h declares,
+and rejects bad arguments with LQ_EINVAL before touching the GPU."""
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "laguna_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from lagunalab_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from lagunalab_amd import build
+        build.build()
+    return _lib.load()
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lq_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = header_functions()
+    for want in ("lq_quantize_append", "lq_dequantize", "lq_decode_attn", "lq_q8_verify_attn",
+                 "lq_ngram_propose", "lq_greedy_accept", "lq_version", "lq_last_error"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from lagunalab_amd import _lib
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(header_functions()) == set(_lib.SIGNATURES), "ctypes table out of sync with header"
+
+
+def test_version(lib):
+    assert lib.lq_version() >= 100
+
+
+def test_quantize_rejects_bad_arguments(lib):
+    from lagunalab_amd import _lib
+    st = lib.lq_quantize_append(1, 1, 8, 1, 128, 1, 1, 1, 256, 0, 5, 64, None)
+    assert st == _lib.LQ_EINVAL and b"bits" in lib.lq_last_error()
+    st = lib.lq_quantize_append(1, 1, 8, 1, 96, 1, 1, 1, 256, 0, 8, 64, None)
+    assert st == _lib.LQ_EINVAL and b"group_size" in lib.lq_last_error()
+    st = lib.lq_quantize_append(1, 1, 8, 4, 128, 1, 1, 1, 256, 254, 8, 64, None)
+    assert st == _lib.LQ_EINVAL and b"capacity" in lib.lq_last_error()
+    st = lib.lq_quantize_append(None, 1, 8, 1, 128, 1, 1, 1, 256, 0, 8, 64, None)
+    assert st == _lib.LQ_EINVAL
+
+
+def test_decode_rejects_bad_arguments(lib):
+    from lagunalab_amd import _lib
+    args = dict(kind=8, q=1, kc=1, ks=1, kb=1, vc=1, vs=1, vb=1, B=1, Hq=32, Hkv=8, D=128,
+                cap=256, n=10, lens=None, scale=0.1, out=1, ws=1, wsb=1 << 20, st=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.lq_decode_attn(*a.values())
+
+    assert call(D=64) == _lib.LQ_EINVAL
+    assert call(Hq=30) == _lib.LQ_EINVAL
+    assert call(Hq=80) == _lib.LQ_EINVAL  # 10 query heads per KV head
+    assert call(B=0) == _lib.LQ_EINVAL
+    assert call(B=65) == _lib.LQ_EINVAL
+    assert call(q=None) == _lib.LQ_EINVAL
+    assert call(kind=3) == _lib.LQ_EINVAL
+
+
+def test_lookup_ops_reject_bad_arguments(lib):
+    from lagunalab_amd import _lib
+    assert lib.lq_ngram_propose(1, 100, 0, 4, 1, 1, 64, None) == _lib.LQ_EINVAL
+    assert lib.lq_ngram_propose(1, 100, 3, 0, 1, 1, 64, None) == _lib.LQ_EINVAL
+    assert lib.lq_greedy_accept(1, 5, 100, 1, 5, 1, 1, 1 << 16, None) == _lib.LQ_EINVAL  # m > L-1
+    assert lib.lq_greedy_accept(1, 0, 100, 1, 0, 1, 1, 1 << 16, None) == _lib.LQ_EINVAL
+
+
+def test_workspace_queries(lib):
+    assert lib.lq_ngram_workspace_bytes(82671) >= 4 * (82671 // 4096)
+    assert lib.lq_accept_workspace_bytes(5, 131072) == 5 * 32 * 8

@@ -1,0 +1,330 @@
+"""GPU parity of liblaguna_hip.so against the CPU oracle, through the Python surface that calls
+the C ABI. Bit-exact for codes, scales, biases, dequantized values, draft ids and accept results;
+attention within max-abs 2e-3 + rel 1e-2 of the unfused dequantize-to-bf16 + SDPA oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import lookup as O
+from oracle import quantize as Q
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2  # attention tolerance (fp32 accumulate, bf16 output)
+
+
+def to_dev_bf16(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev).to(torch.bfloat16)
+
+
+def bits16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def special_rows(D=128):
+    """Groups that stress the quantizer: zeros, constant, ramps, exact halves, tiny values,
+    all-negative, a single outlier."""
+    rows = [np.zeros(D), np.full(D, 0.5), np.arange(D) % 64, -(np.arange(D) % 64),
+            np.tile(np.r_[0, 255, 0.5, 2.5, np.zeros(60)], D // 64),
+            np.tile(np.r_[1.0, -0.3125, np.zeros(62)], D // 64),
+            np.full(D, 3e-8) * np.sign(np.arange(D) % 3 - 1),
+            -np.abs(np.linspace(0.1, 5, D)),
+            np.r_[np.zeros(D - 1), 1000.0]]
+    return Q.round_bf16(np.stack(rows).astype(np.float32))
+
+
+def make_cache(rng, B, Hkv, n, cap, dev, bits=8, D=128):
+    """Random N(0,1) bf16 K/V quantized on the GPU into full-capacity buffers (rows >= n hold
+    garbage codes so a kernel that reads past n is caught)."""
+    out = []
+    for _ in range(2):
+        x = Q.randn_bf16(rng, (B, Hkv, n, D))
+        codes = torch.randint(0, 256, (B, Hkv, cap, D * bits // 8), dtype=torch.uint8, device=dev)
+        sc = to_dev_bf16(rng.standard_normal((B, Hkv, cap, D // 64)) * 100, dev)
+        bi = to_dev_bf16(rng.standard_normal((B, Hkv, cap, D // 64)) * 100, dev)
+        from lagunalab_amd.quant import quantize_into
+        quantize_into(to_dev_bf16(x, dev), codes, sc, bi, 0, 64, bits)
+        out.append((codes, sc, bi))
+    return out
+
+
+def cache_np(c):
+    return tuple(t.cpu().numpy() if t.dtype == torch.uint8 else bits16(t) for t in c)
+
+
+def assert_attn_close(got, want, what=""):
+    got = got.float().cpu().numpy()
+    err = np.abs(got - want)
+    lim = ATOL + RTOL * np.abs(want)
+    assert np.all(err <= lim), f"{what} max-abs {err.max():.3e} (worst excess {(err - lim).max():.3e})"
+
+
+# ---------------------------------------------------------------------------------------------
+# quantize / dequantize: bit-exact
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantize_bit_exact(dev, bits, gs):
+    from lagunalab_amd.quant import quantize
+    rng = np.random.default_rng(10 + bits + gs)
+    x = np.concatenate([Q.randn_bf16(rng, (300, 128)) * np.float32(4), special_rows()])
+    c, s, b = quantize(to_dev_bf16(x, dev), gs, bits)
+    torch.cuda.synchronize()
+    wc, ws, wb = Q.quantize_packed(x, gs, bits)
+    np.testing.assert_array_equal(c.cpu().numpy(), wc)
+    np.testing.assert_array_equal(bits16(s), ws)
+    np.testing.assert_array_equal(bits16(b), wb)
+
+
+def test_quantize_append_writes_only_its_rows(dev):
+    from lagunalab_amd.quant import quantize_into
+    rng = np.random.default_rng(1)
+    B, H, cap, L, off = 2, 3, 64, 5, 17
+    codes = torch.full((B, H, cap, 128), 7, dtype=torch.uint8, device=dev)
+    sc = torch.full((B, H, cap, 2), 1.5, dtype=torch.bfloat16, device=dev)
+    bi = torch.full((B, H, cap, 2), -2.0, dtype=torch.bfloat16, device=dev)
+    x = Q.randn_bf16(rng, (B, H, L, 128))
+    quantize_into(to_dev_bf16(x, dev), codes, sc, bi, off, 64, 8)
+    wc, ws, wb = Q.quantize_packed(x, 64, 8)
+    c = codes.cpu().numpy()
+    np.testing.assert_array_equal(c[:, :, off:off + L], wc)
+    np.testing.assert_array_equal(bits16(sc)[:, :, off:off + L], ws)
+    np.testing.assert_array_equal(bits16(bi)[:, :, off:off + L], wb)
+    assert (c[:, :, :off] == 7).all() and (c[:, :, off + L:] == 7).all()
+    assert (sc[:, :, :off] == 1.5).all() and (bi[:, :, off + L:] == -2.0).all()
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_dequantize_bit_exact(dev, bits):
+    from lagunalab_amd.quant import dequantize
+    rng = np.random.default_rng(2)
+    x = Q.randn_bf16(rng, (2, 4, 70, 128))
+    wc, ws, wb = Q.quantize_packed(x, 64, bits)
+    c = torch.from_numpy(wc).to(dev)
+    s = torch.from_numpy(ws.view(np.int16)).to(dev).view(torch.bfloat16)
+    b = torch.from_numpy(wb.view(np.int16)).to(dev).view(torch.bfloat16)
+    got = dequantize(c, s, b, 64, bits, n=61)
+    want = Q.dequantize(wc[:, :, :61], ws[:, :, :61], wb[:, :, :61], 64, bits)
+    np.testing.assert_array_equal(got.float().cpu().numpy(), want)
+
+
+# ---------------------------------------------------------------------------------------------
+# fused decode attention
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,G,B", [(1, 6, 1), (7, 6, 1), (512, 6, 1), (513, 4, 1), (1636, 6, 1),
+                                   (4096, 4, 1), (300, 1, 2), (777, 2, 1), (2000, 8, 1),
+                                   (1000, 3, 2), (129, 5, 1), (3001, 7, 1)])
+def test_decode_matches_unfused_oracle(dev, n, G, B):
+    from lagunalab_amd.q8_attn import q8_decode_attention
+    rng = np.random.default_rng(n * 10 + G)
+    Hkv = 8
+    cap = (n + 255) // 256 * 256 + (256 if n % 256 == 0 else 0)
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (B, Hkv * G, 1, 128))
+    scale = 128 ** -0.5
+    got = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, n, scale)
+    assert got.shape == (B, Hkv * G, 1, 128) and got.dtype == torch.bfloat16
+    want = A.unfused_attention(q, cache_np(kq), cache_np(vq), n, scale)
+    assert_attn_close(got, want, f"n={n} G={G}")
+
+
+def test_decode_accepts_mlx_word_view_and_other_q_dtypes(dev):
+    from lagunalab_amd.q8_attn import q8_decode_attention
+    rng = np.random.default_rng(3)
+    kq, vq = make_cache(rng, 1, 8, 700, 768, dev)
+    q = Q.randn_bf16(rng, (1, 32, 1, 128))
+    a = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, 700, 0.088)
+    kw = (kq[0].view(torch.int32),) + kq[1:]
+    vw = (vq[0].view(torch.int32),) + vq[1:]
+    b = q8_decode_attention(to_dev_bf16(q, dev), kw, vw, 700, 0.088)
+    torch.testing.assert_close(a, b, rtol=0, atol=0)
+    c = q8_decode_attention(to_dev_bf16(q, dev).float(), kq, vq, 700, 0.088)
+    assert c.dtype == torch.float32
+    torch.testing.assert_close(c, a.float(), rtol=0, atol=0)
+
+
+@pytest.mark.slow
+def test_decode_full_session_length(dev):
+    """Config 2's shape: 82,671 valid rows in an 82,944-row cache, 32q/8kv."""
+    from lagunalab_amd.q8_attn import q8_decode_attention
+    rng = np.random.default_rng(0)
+    n, cap = 82671, 82944
+    kq, vq = make_cache(rng, 1, 8, n, cap, dev)
+    q = Q.randn_bf16(rng, (1, 32, 1, 128))
+    got = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, n, 128 ** -0.5)
+    want = A.unfused_attention(q, cache_np(kq), cache_np(vq), n, 128 ** -0.5)
+    assert_attn_close(got, want, "n=82671")
+
+
+def test_ragged_matches_per_sequence_oracle(dev):
+    from lagunalab_amd.q8_attn import decode_attention
+    rng = np.random.default_rng(1)
+    lens = [61, 1, 2048, 513, 3000, 256, 1000, 4095]
+    B, cap = len(lens), 4096
+    kq, vq = make_cache(rng, B, 8, cap, cap, dev)
+    q = Q.randn_bf16(rng, (B, 32, 1, 128))
+    got = decode_attention(to_dev_bf16(q, dev), kq, vq, lens=lens, scale=128 ** -0.5)
+    want = A.ragged_unfused_attention(q, cache_np(kq), cache_np(vq), lens, 128 ** -0.5)
+    assert_attn_close(got, want, "ragged")
+
+
+def test_ragged_session_lengths_match_single_calls(dev):
+    """Config 3's lengths (default_rng(1) in [42771, 82671]): the variable-length call equals one
+    call per sequence (size-independent property; per-sequence calls are checked above)."""
+    from lagunalab_amd.q8_attn import decode_attention
+    lens = [int(x) for x in np.random.default_rng(1).integers(42771, 82672, size=8)]
+    cap = 82944
+    g = torch.Generator(device=dev).manual_seed(0)
+    kq = (torch.randint(0, 256, (8, 8, cap, 128), dtype=torch.uint8, device=dev, generator=g),
+          (torch.rand(8, 8, cap, 2, device=dev, generator=g) * 0.03).to(torch.bfloat16),
+          (torch.rand(8, 8, cap, 2, device=dev, generator=g) * -3).to(torch.bfloat16))
+    vq = (torch.randint(0, 256, (8, 8, cap, 128), dtype=torch.uint8, device=dev, generator=g),
+          (torch.rand(8, 8, cap, 2, device=dev, generator=g) * 0.03).to(torch.bfloat16),
+          (torch.rand(8, 8, cap, 2, device=dev, generator=g) * -3).to(torch.bfloat16))
+    q = torch.randn(8, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
+    got = decode_attention(q, kq, vq, lens=lens, scale=128 ** -0.5)
+    for b, n in enumerate(lens):
+        one = decode_attention(q[b:b + 1], tuple(t[b:b + 1] for t in kq),
+                               tuple(t[b:b + 1] for t in vq), n=n, scale=128 ** -0.5)
+        torch.testing.assert_close(got[b:b + 1].float(), one.float(), atol=1e-3, rtol=1e-2)
+
+
+# ---------------------------------------------------------------------------------------------
+# n-gram propose and greedy accept: bit-exact
+# ---------------------------------------------------------------------------------------------
+
+def planted_history(T=82671, seed=0):
+    rng = np.random.default_rng(seed)
+    h = rng.integers(0, 131072, size=T).astype(np.int32)
+    for s in range(0, T - 600, 500):  # copy an 8-gram forward every ~500 tokens
+        src = rng.integers(0, max(1, s - 8)) if s > 8 else 0
+        h[s:s + 8] = h[src:src + 8]
+    h[-3:] = h[T // 2:T // 2 + 3]  # make the final 3-gram occur earlier
+    return h
+
+
+@pytest.mark.parametrize("T,g,n", [(82671, 3, 4), (82671, 4, 7), (5000, 1, 15), (20, 3, 4),
+                                   (3, 3, 4), (2, 3, 4), (0, 3, 4), (4, 3, 4)])
+def test_ngram_propose_bit_exact(dev, T, g, n):
+    from lagunalab_amd.lookup import ngram_propose
+    h = planted_history(max(T, 1))[:T] if T >= 100 else np.random.default_rng(T).integers(0, 3, T).astype(np.int32)
+    hist = torch.from_numpy(np.ascontiguousarray(h)).to(dev) if T else torch.zeros(1, dtype=torch.int32, device=dev)
+    out = ngram_propose(hist, T, g, n).cpu().numpy()
+    cnt, pos, ids = O.propose_scan(h, T, g, n)
+    assert int(out[0]) == cnt and int(out[1]) == pos
+    assert out[2:2 + cnt].tolist() == ids
+    assert ids == O.lookup(h.tolist(), T, g, n)
+
+
+def test_ngram_edge_cases(dev):
+    from lagunalab_amd.lookup import ngram_propose
+    cases = [
+        [7] * 6,                                   # overlapping match at s = T-g-1
+        [1, 2, 3, 10, 1, 2, 3, 20, 5, 1, 2, 3],    # most recent match wins
+        [1, 2, 3, 4, 5, 6, 7],                     # no match
+        [5, 6, 7, 8, 5, 6, 7],                     # continuation truncated at T
+    ]
+    for seq in cases:
+        h = torch.tensor(seq, dtype=torch.int32, device=dev)
+        for g in (1, 2, 3):
+            out = ngram_propose(h, len(seq), g, 4).cpu().numpy()
+            want = O.lookup(seq, len(seq), g, 4)
+            assert out[0] == len(want) and out[2:2 + len(want)].tolist() == want, (seq, g)
+
+
+def test_device_index_matches_host_index(dev):
+    from lagunalab_amd.lookup import DeviceNgramIndex, NgramIndex
+    seq = [int(t) for t in np.random.default_rng(1).integers(0, 5, size=120)]
+    a, b = NgramIndex(3), DeviceNgramIndex(3, dev, capacity=16)
+    for t in range(len(seq)):
+        assert a.propose(7) == b.propose(7)
+        a.extend(seq[t:t + 1])
+        b.extend(seq[t:t + 1])
+
+
+@pytest.mark.parametrize("m", [0, 1, 2, 3, 4])
+def test_greedy_accept_bit_exact(dev, m):
+    from lagunalab_amd.lookup import greedy_accept
+    rng = np.random.default_rng(m)
+    logits = rng.standard_normal((5, 131072)).astype(np.float32)
+    pred = logits.argmax(-1)
+    drafts = np.array(list(pred[:m]) + [int(pred[m]) ^ 1] * (4 - m), np.int32)
+    out = greedy_accept(torch.from_numpy(logits).to(dev), torch.from_numpy(drafts).to(dev)).cpu().numpy()
+    k, nxt = O.greedy_accept(logits, drafts)
+    assert int(out[0]) == k == m and int(out[1]) == nxt
+    assert out[2:].tolist() == pred.tolist()
+
+
+def test_greedy_accept_ties_and_odd_vocab(dev):
+    from lagunalab_amd.lookup import greedy_accept
+    logits = np.zeros((3, 10007), np.float32)
+    logits[0, [9000, 17, 5000]] = 3.0   # first index (17) wins
+    logits[1, [10006, 4096]] = 1.0      # across chunk boundary: 4096
+    logits[2, :] = -1.0
+    logits[2, 10006] = 0.0
+    drafts = np.array([17, 4096], np.int32)
+    out = greedy_accept(torch.from_numpy(logits).to(dev), torch.from_numpy(drafts).to(dev)).cpu().numpy()
+    assert out.tolist() == [2, 10006, 17, 4096, 10006]
+
+
+# ---------------------------------------------------------------------------------------------
+# cache semantics on the GPU
+# ---------------------------------------------------------------------------------------------
+
+def test_quantized_cache_chunked_matches_one_pass(dev):
+    """tests/test_cache.py:117-123's split: 200 + 60 rows, then 40 single rows, across the
+    256-row growth step; the valid rows are bit-identical to one 300-row append."""
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(5)
+    k = to_dev_bf16(Q.randn_bf16(rng, (1, 2, 300, 64)), dev)
+    v = to_dev_bf16(Q.randn_bf16(rng, (1, 2, 300, 64)), dev)
+    one = DequantKVCache(bits=8)
+    ko, vo = one.update_and_fetch(k, v)
+    c = DequantKVCache(bits=8)
+    caps = []
+    for a, b in [(0, 200), (200, 260)] + [(i, i + 1) for i in range(260, 300)]:
+        kc, vc = c.update_and_fetch(k[:, :, a:b], v[:, :, a:b])
+        caps.append(c.q.keys[0].shape[2])
+    assert caps[0] == 256 and caps[1] == 456  # trimmed to 200, then one 256-row step
+    assert c.offset == one.offset == 300
+    torch.testing.assert_close(kc, ko, rtol=0, atol=0)
+    torch.testing.assert_close(vc, vo, rtol=0, atol=0)
+    for x, y in zip(c.state[0], one.state[0]):
+        torch.testing.assert_close(x, y, rtol=0, atol=0)
+
+
+def test_dequant_cache_switches(dev):
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(6)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 2, L, 64)), dev)
+    c = DequantKVCache(bits=8, quantized_decode=True)
+    k, _ = c.update_and_fetch(kv(5), kv(5))
+    assert torch.is_tensor(k) and not hasattr(c, "bits")
+    k, _ = c.update_and_fetch(kv(1), kv(1))
+    assert isinstance(k, tuple) and c.bits == 8
+    off = DequantKVCache(bits=8)
+    off.update_and_fetch(kv(1), kv(1))
+    assert not hasattr(off, "bits")
+    assert c.trim(3) == 3 and c.offset == 3 and c.nbytes > 0
+
+
+def test_fused_step_matches_dequantized_path(dev):
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(7)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 8, L, 128)), dev)
+    fused, plain = DequantKVCache(fused_decode=True), DequantKVCache()
+    k0, v0 = kv(600), kv(600)
+    fused.update_and_fetch(k0, v0)
+    plain.update_and_fetch(k0, v0)
+    k1, v1 = kv(1), kv(1)
+    fused.update_and_fetch(k1, v1)
+    K, V = plain.update_and_fetch(k1, v1)
+    assert fused.fused_step and not plain.fused_step
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 1, 128)), dev)
+    got = fused.attend(q, 128 ** -0.5)
+    qn = q.float().cpu().numpy()
+    want = A.sdpa(qn, K.float().cpu().numpy(), V.float().cpu().numpy(), 128 ** -0.5)
+    assert_attn_close(got, want.astype(np.float32), "fused vs dequantized")
