@@ -115,36 +115,47 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
       qsum[h] = a;
     }
     const uint8_t* kbase = kc + row0 * D + 32 * rl;
-    const uint16_t* ksb = ks + row0 * 2 + kgrp;
-    const uint16_t* kbb = kb + row0 * 2 + kgrp;
+    // scale/bias of both groups of a row as one 32-bit word (group kgrp picked at use)
+    const uint32_t* ksw = reinterpret_cast<const uint32_t*>(ks + row0 * 2);
+    const uint32_t* kbw = reinterpret_cast<const uint32_t*>(kb + row0 * 2);
+    const int kshift = 16 * kgrp;
 
-    for (int j = 0; j <= ntiles; ++j) {
+    // Branch-free loads (rows past the tile end are clamped to its last row and masked later),
+    // issued one tile ahead of their use so every wave keeps a tile of loads in flight.
+    uint4 ca[4], cb[4];
+    uint32_t sraw[4], braw[4];
+    auto load_tile = [&](int jt, uint4* xa, uint4* xb, uint32_t* xs, uint32_t* xbias) {
+      const int t0 = t_begin + jt * KT;
+      const int last = min(KT, t_end - t0) - 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t t = t0 + min(64 * wv + 16 * i + rsub, last);
+        xs[i] = ksw[t];
+        xbias[i] = kbw[t];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t t = t0 + min(64 * wv + 16 * i + rsub, last);
+        const uint4* p = reinterpret_cast<const uint4*>(kbase + t * D);
+        xa[i] = p[0];
+        xb[i] = p[1];
+      }
+    };
+    load_tile(0, ca, cb, sraw, braw);
+
+    // One pipeline step: prefetch tile j+1 into (xa..), score tile j from (ya..), barrier.
+    auto step = [&](int j, const uint4* ya, const uint4* yb, const uint32_t* ys,
+                    const uint32_t* ybias, uint4* xa, uint4* xb, uint32_t* xs, uint32_t* xbias) {
+      if (j + 1 < ntiles) load_tile(j + 1, xa, xb, xs, xbias);
       if (j < ntiles) {
         const int t0 = t_begin + j * KT;
         const int rows = min(KT, t_end - t0);
-        uint4 ca[4], cb[4];
-        float sc[4], bi[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 64 * wv + 16 * i + rsub;
-          if (r < rows) {
-            const int64_t t = t0 + r;
-            const uint4* p = reinterpret_cast<const uint4*>(kbase + t * D);
-            ca[i] = p[0];
-            cb[i] = p[1];
-            sc[i] = bf16_to_f32(ksb[2 * t]);
-            bi[i] = bf16_to_f32(kbb[2 * t]);
-          } else {
-            ca[i] = cb[i] = make_uint4(0, 0, 0, 0);
-            sc[i] = bi[i] = 0.0f;
-          }
-        }
         float(*S)[G] = sm.s[j & 1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 64 * wv + 16 * i + rsub;
-          const uint32_t wd[8] = {ca[i].x, ca[i].y, ca[i].z, ca[i].w,
-                                  cb[i].x, cb[i].y, cb[i].z, cb[i].w};
+          const uint32_t wd[8] = {ya[i].x, ya[i].y, ya[i].z, ya[i].w,
+                                  yb[i].x, yb[i].y, yb[i].z, yb[i].w};
           float dacc[G];
 #pragma unroll
           for (int h = 0; h < G; ++h) dacc[h] = 0.0f;
@@ -159,8 +170,10 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
             }
           }
           // q.(s c + b) = s (q.(1024 + c)) + (b - 1024 s) sum(q), times scale*log2(e)
-          const float s1 = sc[i] * qk_scale_log2;
-          const float u1 = (bi[i] - 1024.0f * sc[i]) * qk_scale_log2;
+          const float sc = bf16_to_f32((uint16_t)(ys[i] >> kshift));
+          const float bi = bf16_to_f32((uint16_t)(ybias[i] >> kshift));
+          const float s1 = sc * qk_scale_log2;
+          const float u1 = (bi - 1024.0f * sc) * qk_scale_log2;
 #pragma unroll
           for (int h = 0; h < G; ++h) {
             const float part = quad_sum(s1 * dacc[h] + u1 * qsum[h]);
@@ -169,6 +182,12 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
         }
       }
       __syncthreads();
+    };
+    uint4 na[4], nb[4];
+    uint32_t ns[4], nbias[4];
+    for (int j = 0; j <= ntiles; j += 2) {
+      step(j, ca, cb, sraw, braw, na, nb, ns, nbias);
+      if (j + 1 <= ntiles) step(j + 1, na, nb, ns, nbias, ca, cb, sraw, braw);
     }
   } else {
     // ================================ consumer: softmax + P.V ==============================
@@ -193,33 +212,48 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
       lsum[h] = wsum[h] = bsum[h] = 0.0f;
     }
     const uint8_t* vbase = vc + row0 * D + 16 * vl;
-    const uint16_t* vsb = vs + row0 * 2 + sg;
-    const uint16_t* vbb = vb + row0 * 2 + sg;
+    const uint32_t* vsw = reinterpret_cast<const uint32_t*>(vs + row0 * 2);
+    const uint32_t* vbw = reinterpret_cast<const uint32_t*>(vb + row0 * 2);
+    const int vshift = 16 * sg;
     half2_t(*W)[2][G] = sm.w[cw];
 
-    for (int j = 0; j <= ntiles; ++j) {
+    // V codes of 4 row pairs per lane plus the softmax rows' V scale/bias, loaded branch-free
+    // (rows clamped to the tile's last row) one tile ahead of their use.
+    uint4 ca[4], cb[4];
+    uint32_t vraw[4];  // scale and bias words (both groups) of rows sr0, sr1
+    auto load_tile = [&](int jt, uint4* xa, uint4* xb, uint32_t* xr) {
+      const int t0 = t_begin + jt * KT;
+      const int last = min(KT, t_end - t0) - 1;
+      const int64_t u0 = t0 + min(sr0, last), u1 = t0 + min(sr1, last);
+      xr[0] = vsw[u0];
+      xr[1] = vsw[u1];
+      xr[2] = vbw[u0];
+      xr[3] = vbw[u1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = min(64 * cw + 16 * i + rs, last);
+        const int r1 = min(64 * cw + 16 * i + rs + 8, last);
+        xa[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(t0 + r0) * D);
+        xb[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(t0 + r1) * D);
+      }
+    };
+    if (ntiles > 0) load_tile(0, ca, cb, vraw);
+
+    // One pipeline step: prefetch tile j into (xa..), softmax + P.V of tile j-1 from (ya..).
+    auto step = [&](int j, const uint4* ya, const uint4* yb, const uint32_t* yr, uint4* xa,
+                    uint4* xb, uint32_t* xr) {
       if (j >= 1) {
         const int jt = j - 1;
         const int t0 = t_begin + jt * KT;
         const int rows = min(KT, t_end - t0);
-        // issue the tile's V code loads first
-        uint4 ca[4], cb[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r0 = 64 * cw + 16 * i + rs;
-          const int r1 = r0 + 8;
-          ca[i] = r0 < rows ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(t0 + r0) * D)
-                            : make_uint4(0, 0, 0, 0);
-          cb[i] = r1 < rows ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(t0 + r1) * D)
-                            : make_uint4(0, 0, 0, 0);
-        }
+        if (j < ntiles) load_tile(j, xa, xb, xr);
         // softmax over this wave's 64 rows
         const float(*S)[G] = sm.s[jt & 1];
         const bool ok0 = sr0 < rows, ok1 = sr1 < rows;
-        const float vs0 = ok0 ? bf16_to_f32(vsb[2 * (int64_t)(t0 + sr0)]) : 0.0f;
-        const float vs1 = ok1 ? bf16_to_f32(vsb[2 * (int64_t)(t0 + sr1)]) : 0.0f;
-        const float vb0 = ok0 ? bf16_to_f32(vbb[2 * (int64_t)(t0 + sr0)]) : 0.0f;
-        const float vb1 = ok1 ? bf16_to_f32(vbb[2 * (int64_t)(t0 + sr1)]) : 0.0f;
+        const float vs0 = ok0 ? bf16_to_f32((uint16_t)(yr[0] >> vshift)) : 0.0f;
+        const float vs1 = ok1 ? bf16_to_f32((uint16_t)(yr[1] >> vshift)) : 0.0f;
+        const float vb0 = ok0 ? bf16_to_f32((uint16_t)(yr[2] >> vshift)) : 0.0f;
+        const float vb1 = ok1 ? bf16_to_f32((uint16_t)(yr[3] >> vshift)) : 0.0f;
         float alpha[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -246,11 +280,12 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
           for (int d = 0; d < 16; ++d) acc[h][d] *= alpha[h];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          // rows past the tile end carry weight 0 (their scores are -inf)
           half2_t wt[G];
 #pragma unroll
           for (int h = 0; h < G; ++h) wt[h] = W[8 * i + rs][vgrp][h];
-          const uint32_t w0[4] = {ca[i].x, ca[i].y, ca[i].z, ca[i].w};
-          const uint32_t w1[4] = {cb[i].x, cb[i].y, cb[i].z, cb[i].w};
+          const uint32_t w0[4] = {ya[i].x, ya[i].y, ya[i].z, ya[i].w};
+          const uint32_t w1[4] = {yb[i].x, yb[i].y, yb[i].z, yb[i].w};
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             // interleave two rows' bytes: xl = (a0, b0, a1, b1), xh = (a2, b2, a3, b3)
@@ -271,6 +306,14 @@ __global__ __launch_bounds__(NT) void q8_decode_split_kernel(
         }
       }
       __syncthreads();
+    };
+    uint4 na[4], nb[4];
+    uint32_t nr[4];
+    // iteration j consumes the buffer tile j-1 was loaded into: tile t lives in (ca..) for even
+    // t and in (na..) for odd t
+    for (int j = 0; j <= ntiles; j += 2) {
+      step(j, na, nb, nr, ca, cb, vraw);  // j even: consumes tile j-1 (odd), loads tile j (even)
+      if (j + 1 <= ntiles) step(j + 1, ca, cb, vraw, na, nb, nr);
     }
 
     // ---- consumer wave partial: sum acc over the 8 row slots, the softmax sums over lanes
@@ -347,20 +390,51 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
                                                          const float2* __restrict__ part_ml,
                                                          int Hq, DecodePlan plan,
                                                          uint16_t* __restrict__ out) {
+  constexpr int MAXS = 1024;  // splits merged per pass through LDS
+  __shared__ float wsh[MAXS];
+  __shared__ float red[2];
   const int bq = blockIdx.x;
   const int b = bq / Hq;
   const int hq = bq - b * Hq;
   const int d = threadIdx.x;
   const int s0 = plan.split_begin[b], s1 = plan.split_begin[b + 1];
+  // global max over the sequence's splits: all threads load (m, l) in parallel
   float M = -INFINITY;
-  for (int s = s0; s < s1; ++s) M = fmaxf(M, part_ml[(int64_t)s * Hq + hq].x);
+  for (int s = s0 + d; s < s1; s += D) M = fmaxf(M, part_ml[(int64_t)s * Hq + hq].x);
+  M = wave_max(M);
+  if ((d & 63) == 0) red[d >> 6] = M;
+  __syncthreads();
+  M = fmaxf(red[0], red[1]);
   float num = 0.0f, den = 0.0f;
-  for (int s = s0; s < s1; ++s) {
-    const float2 ml = part_ml[(int64_t)s * Hq + hq];
-    const float w = exp2f(ml.x - M);
-    den += w * ml.y;
-    num += w * part_acc[((int64_t)s * Hq + hq) * D + d];
+  for (int c0 = s0; c0 < s1; c0 += MAXS) {
+    const int c1 = min(s1, c0 + MAXS);
+    __syncthreads();
+    for (int s = c0 + d; s < c1; s += D) {
+      const float2 ml = part_ml[(int64_t)s * Hq + hq];
+      const float w = exp2f(ml.x - M);
+      wsh[s - c0] = w;
+      den += w * ml.y;
+    }
+    __syncthreads();
+    const float* pa = part_acc + ((int64_t)c0 * Hq + hq) * D + d;
+    const int cnt = c1 - c0;
+    int s = 0;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (; s + 4 <= cnt; s += 4) {
+      a0 += wsh[s] * pa[(int64_t)s * Hq * D];
+      a1 += wsh[s + 1] * pa[(int64_t)(s + 1) * Hq * D];
+      a2 += wsh[s + 2] * pa[(int64_t)(s + 2) * Hq * D];
+      a3 += wsh[s + 3] * pa[(int64_t)(s + 3) * Hq * D];
+    }
+    for (; s < cnt; ++s) a0 += wsh[s] * pa[(int64_t)s * Hq * D];
+    num += (a0 + a1) + (a2 + a3);
   }
+  // den: each thread summed a strided subset of the splits
+  den = wave_sum(den);
+  __syncthreads();
+  if ((d & 63) == 0) red[d >> 6] = den;
+  __syncthreads();
+  den = red[0] + red[1];
   out[((int64_t)b * Hq + hq) * D + d] = f32_to_bf16(num / den);
 }
 

@@ -13,6 +13,10 @@ What it restates.
   ``0 .. n - L + i`` (``laguna.py:183-186``; pinned by ``tests/test_cache.py:23-28``). The math
   runs in float64; the result is returned as fp32 (callers round to bf16 when comparing a bf16
   output).
+* :func:`fused_attention` -- the same attention with the fused kernel's dequantization (fp32
+  ``scale * code + bias``, no bf16 rounding; ``q8_attn.py:46-55``). The two paths differ by the
+  bf16 rounding of K/V: negligible once thousands of keys are averaged, up to ~1e-2 with a handful
+  of keys (the reference's own fused-vs-unfused test allows 2e-2, ``tests/test_q8_attn.py:31``).
 * :func:`block_partials` / :func:`merge_partials` -- the fused kernel's flash-decoding split:
   per block of keys the running max ``m``, the sum ``l`` of ``exp(s - m)`` and the unnormalised
   ``acc = sum exp(s - m) v`` (``q8_attn.py:44-91``), then the log-sum-exp merge
@@ -68,21 +72,34 @@ def unfused_attention(q, kcache, vcache, n, scale, bits=8, group_size=64, causal
     return sdpa(q, k, v, scale, causal=causal).astype(np.float32)
 
 
+def fused_attention(q, kcache, vcache, n, scale, bits=8, group_size=64, causal=True):
+    """The reference's fused-kernel arithmetic: K/V dequantized as ``scale * code + bias`` in fp32
+    without rounding to bf16 (``q8_attn.py:46-55``), then exact softmax attention (float64).
+    Same arguments as :func:`unfused_attention`."""
+    kc, ks, kb = (a[:, :, :n] for a in kcache)
+    vc, vs, vb = (a[:, :, :n] for a in vcache)
+    k = dequantize_f32(kc, ks, kb, group_size, bits)
+    v = dequantize_f32(vc, vs, vb, group_size, bits)
+    return sdpa(q, k, v, scale, causal=causal).astype(np.float32)
+
+
 def bf16_attention(q, k, v, n, scale, causal=True):
     """Plain bf16 cache (values already bf16-exact fp32 [B,Hkv,cap,D])."""
     return sdpa(q, k[:, :, :n], v[:, :, :n], scale, causal=causal).astype(np.float32)
 
 
-def ragged_unfused_attention(q, kcache, vcache, lens, scale, bits=8, group_size=64):
+def ragged_unfused_attention(q, kcache, vcache, lens, scale, bits=8, group_size=64, fused=False):
     """One call per sequence, as the reference must do (``q8_attn.py:102`` takes one ``n``).
 
-    q [B, Hq, 1, D]; caches [B, Hkv, cap, .]; lens: B valid lengths."""
+    q [B, Hq, 1, D]; caches [B, Hkv, cap, .]; lens: B valid lengths. ``fused`` selects the
+    fp32-dequantize arithmetic of :func:`fused_attention`."""
+    fn = fused_attention if fused else unfused_attention
     out = []
     for b, n in enumerate(lens):
         qb = q[b:b + 1]
         kb = tuple(a[b:b + 1] for a in kcache)
         vb = tuple(a[b:b + 1] for a in vcache)
-        out.append(unfused_attention(qb, kb, vb, int(n), scale, bits, group_size))
+        out.append(fn(qb, kb, vb, int(n), scale, bits, group_size))
     return np.concatenate(out, axis=0)
 
 
