@@ -1,0 +1,45 @@
+// Shared declarations of the split-K attention kernels: the per-call split plan and the entry
+// points of the MFMA kernels (qattn.hip) used by the decode and verify C ABI (decode.hip,
+// verify.hip).
+#pragma once
+
+#include "common.h"
+
+namespace lq {
+
+constexpr int D = 128;  // head_dim of the fused kernels
+
+// Variable-length split plan, passed by value as a kernel argument. Sequence b owns the global
+// splits [split_begin[b], split_begin[b+1]); split s of it covers keys
+// [s * chunk, min((s + 1) * chunk, len[b])).
+struct DecodePlan {
+  int32_t nseq;
+  int32_t chunk;
+  int32_t split_begin[LQ_MAX_SEQS + 1];
+  int32_t len[LQ_MAX_SEQS];
+};
+
+__device__ __forceinline__ void find_seq(const DecodePlan& plan, int x, int& b) {
+  b = 0;
+  for (int i = 1; i < plan.nseq; ++i)
+    if (x >= plan.split_begin[i]) b = i;
+}
+
+typedef void (*QAttnFn)(const uint16_t*, const uint8_t*, const uint16_t*, const uint16_t*,
+                        const uint8_t*, const uint16_t*, const uint16_t*, int, int, int, int64_t,
+                        float, DecodePlan, float*, float2*);
+
+// MFMA attention kernel for `nt` 16-column tiles of query rows (G * L <= 16 * nt), causal for
+// multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4.
+QAttnFn q8_attn_fn(int nt, bool causal);
+
+// Plan + workspace bytes for an attention call with L query rows per head; returns the number
+// of splits (or -1) and selects the kernel.
+int64_t attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n, const int32_t* lens,
+                  int64_t cap, DecodePlan& plan, QAttnFn& fn, int64_t& ws_bytes);
+
+// Per-sequence log-sum-exp merge of split partials: rows_per_seq = Hq * L partial rows per split.
+void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq,
+                  const DecodePlan& plan, int64_t B, uint16_t* out, hipStream_t st);
+
+}  // namespace lq

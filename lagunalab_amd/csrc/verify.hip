@@ -1,11 +1,30 @@
 // Multi-query causal verify attention over the 8-bit cache (speculative-decoding verify step).
+//
+// Replaces the verify forward's attention of the reference's speculative loop
+// (laguna_mlx/dflash.py:195) over DequantKVCache's dequantized K/V (cache.py:99-100) with the
+// bottom-right causal mask (laguna.py:107, 183-186): the L query rows of each head are the
+// block's own last L keys, and row i sees keys 0 .. n-L+i. Same MFMA kernel as decode
+// (qattn.hip), with the G*L query rows of a KV head as the MFMA columns and the causal bound
+// applied per column.
 #include "common.h"
+#include "qattn.h"
 
 extern "C" int64_t lq_verify_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
                                              int64_t D, int64_t n) {
-  (void)B; (void)Hq; (void)Hkv; (void)L; (void)D; (void)n;
-  lq::set_error("lq_q8_verify_attn is not built yet");
-  return -1;
+  using namespace lq;
+  clear_error();
+  if (D != 128 || Hkv < 1 || Hq % Hkv || L < 1 || L > 16 || (Hq / Hkv) * L > 64) {
+    set_error("unsupported verify configuration");
+    return -1;
+  }
+  DecodePlan plan;
+  QAttnFn fn;
+  int64_t ws = 0;
+  if (attn_plan(B, Hq, Hkv, L, n, nullptr, 0, plan, fn, ws) < 0) {
+    set_error("bad sequence length");
+    return -1;
+  }
+  return ws;
 }
 
 extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uint16_t* ks,
@@ -13,9 +32,36 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
                                  const uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
                                  int64_t D, int64_t cap, int64_t n, float scale, uint16_t* out,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  (void)q; (void)kc; (void)ks; (void)kb; (void)vc; (void)vs; (void)vb; (void)B; (void)Hq;
-  (void)Hkv; (void)L; (void)D; (void)cap; (void)n; (void)scale; (void)out; (void)workspace;
-  (void)workspace_bytes; (void)stream;
-  lq::set_error("lq_q8_verify_attn is not built yet");
-  return LQ_EINVAL;
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(D == 128, "head_dim must be 128 (got %lld)", (long long)D);
+  LQ_CHECK_ARG(L >= 1 && L <= 16, "verify block of %lld rows outside [1, 16]", (long long)L);
+  LQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "Hq=%lld must be a multiple of Hkv=%lld",
+               (long long)Hq, (long long)Hkv);
+  LQ_CHECK_ARG((Hq / Hkv) * L <= 64, "G * L = %lld query rows per KV head exceed 64",
+               (long long)((Hq / Hkv) * L));
+  LQ_CHECK_ARG(B >= 1 && B <= LQ_MAX_SEQS, "batch %lld outside [1, %d]", (long long)B, LQ_MAX_SEQS);
+  LQ_CHECK_ARG(n >= L && n <= cap && cap <= INT32_MAX, "n=%lld must be in [L, cap=%lld]",
+               (long long)n, (long long)cap);
+  LQ_CHECK_ARG(q && kc && ks && kb && vc && vs && vb && out, "null pointer");
+  DecodePlan plan;
+  QAttnFn fn;
+  int64_t need = 0;
+  const int64_t S = attn_plan(B, Hq, Hkv, L, n, nullptr, cap, plan, fn, need);
+  LQ_CHECK_ARG(S > 0, "bad sequence length");
+  if (!workspace || workspace_bytes < need) {
+    set_error("workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
+              (long long)need);
+    return LQ_EWORKSPACE;
+  }
+  float* part_acc = reinterpret_cast<float*>(workspace);
+  float2* part_ml = reinterpret_cast<float2*>(part_acc + S * Hq * L * D);
+  hipStream_t st = (hipStream_t)stream;
+  const float qk = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, q, kc, ks, kb, vc,
+                     vs, vb, (int)Hkv, (int)(Hq / Hkv), (int)L, cap, qk, plan, part_acc, part_ml);
+  LQ_CHECK_LAUNCH("q8_attn_mfma_kernel");
+  launch_merge(part_acc, part_ml, (int)(Hq * L), plan, B, out, st);
+  LQ_CHECK_LAUNCH("decode_merge_kernel");
+  return LQ_OK;
 }

@@ -138,7 +138,7 @@ def q8_decode_attention(q, keys, values, n, scale):
         raise AssertionError("8-bit, group_size 64 only")
     hkv = codes.shape[1]
     G = Hq // hkv
-    if G > 8 or Hq % hkv:
+    if G > 16 or Hq % hkv:
         raise AssertionError(f"{G} q heads per kv head is too many for one workgroup")
     out = decode_attention(q.to(torch.bfloat16), keys, values, n=int(n), scale=scale)
     return out.to(q.dtype)

@@ -65,7 +65,7 @@ def test_decode_rejects_bad_arguments(lib):
 
     assert call(D=64) == _lib.LQ_EINVAL
     assert call(Hq=30) == _lib.LQ_EINVAL
-    assert call(Hq=80) == _lib.LQ_EINVAL  # 10 query heads per KV head
+    assert call(Hq=136) == _lib.LQ_EINVAL  # 17 query heads per KV head
     assert call(B=0) == _lib.LQ_EINVAL
     assert call(B=65) == _lib.LQ_EINVAL
     assert call(q=None) == _lib.LQ_EINVAL

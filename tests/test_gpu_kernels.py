@@ -346,3 +346,72 @@ def test_fused_step_matches_dequantized_path(dev):
     qn = q.float().cpu().numpy()
     want = A.sdpa(qn, K.float().cpu().numpy(), V.float().cpu().numpy(), 128 ** -0.5)
     assert_attn_close(got, want.astype(np.float32), "fused vs dequantized", REF_SMALL_N_ATOL, 0.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# fused causal verify attention (speculative-decoding block)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,L,G", [(4101, 5, 4), (600, 2, 6), (1000, 8, 2), (300, 16, 4),
+                                   (37, 5, 4), (16, 16, 1), (5000, 3, 8)])
+def test_verify_matches_causal_oracle(dev, n, L, G):
+    from lagunalab_amd.q8_attn import q8_verify_attention
+    rng = np.random.default_rng(n + 7 * L + G)
+    Hkv = 8
+    cap = (n + 255) // 256 * 256
+    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (1, Hkv * G, L, 128))
+    scale = 128 ** -0.5
+    got = q8_verify_attention(to_dev_bf16(q, dev), kq, vq, n, scale)
+    assert got.shape == (1, Hkv * G, L, 128) and got.dtype == torch.bfloat16
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, scale, causal=True),
+                      f"fused verify n={n} L={L} G={G}")
+    at, rt = unfused_tol(n)
+    assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale, causal=True),
+                      f"unfused verify n={n} L={L} G={G}", at, rt)
+
+
+def test_verify_single_row_equals_decode(dev):
+    from lagunalab_amd.q8_attn import q8_decode_attention, q8_verify_attention
+    rng = np.random.default_rng(11)
+    kq, vq = make_cache(rng, 1, 8, 2000, 2048, dev)
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 1, 128)), dev)
+    a = q8_decode_attention(q, kq, vq, 2000, 0.09)
+    b = q8_verify_attention(q, kq, vq, 2000, 0.09)
+    torch.testing.assert_close(a.float(), b.float(), atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.slow
+def test_verify_session_shape(dev):
+    """Config 4a's shape: 65,536 cached keys + a 5-row block (1 accepted + 4 drafts), 32q/8kv."""
+    from lagunalab_amd.q8_attn import q8_verify_attention
+    rng = np.random.default_rng(4)
+    n, L = 65536 + 5, 5
+    kq, vq = make_cache(rng, 1, 8, n, 65536 + 256, dev)
+    q = Q.randn_bf16(rng, (1, 32, L, 128))
+    got = q8_verify_attention(to_dev_bf16(q, dev), kq, vq, n, 128 ** -0.5)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.unfused_attention(q, kn, vn, n, 128 ** -0.5, causal=True), "verify 65541")
+
+
+def test_fused_verify_step_in_cache(dev):
+    """DequantKVCache(fused_decode=True) takes a 5-row block through the fused verify kernel;
+    the result matches attention over the dequantized path with the causal mask."""
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(12)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 8, L, 128)), dev)
+    fused, plain = DequantKVCache(fused_decode=True), DequantKVCache()
+    k0, v0 = kv(700), kv(700)
+    fused.update_and_fetch(k0, v0)
+    plain.update_and_fetch(k0, v0)
+    k1, v1 = kv(5), kv(5)
+    fused.update_and_fetch(k1, v1)
+    K, V = plain.update_and_fetch(k1, v1)
+    assert fused.fused_step and not plain.fused_step
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 5, 128)), dev)
+    got = fused.attend(q, 128 ** -0.5)
+    want = A.sdpa(q.float().cpu().numpy(), K.float().cpu().numpy(), V.float().cpu().numpy(),
+                  128 ** -0.5, causal=True)
+    assert_attn_close(got, want.astype(np.float32), "fused verify vs dequantized",
+                      REF_SMALL_N_ATOL, 0.0)

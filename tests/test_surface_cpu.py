@@ -48,7 +48,7 @@ def test_q8_decode_attention_assertions():
     with pytest.raises(AssertionError, match="8-bit"):
         QA.q8_decode_attention(torch.zeros(1, 32, 1, 128, dtype=torch.bfloat16), kv4, kv4, 10, 0.1)
     with pytest.raises(AssertionError, match="too many"):
-        QA.q8_decode_attention(torch.zeros(1, 80, 1, 128, dtype=torch.bfloat16), kv, kv, 10, 0.1)
+        QA.q8_decode_attention(torch.zeros(1, 136, 1, 128, dtype=torch.bfloat16), kv, kv, 10, 0.1)
 
 
 def test_no_cpu_path():
