@@ -27,7 +27,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "q8 decode-attn µs/call & HBM GB/s (% of 8 TB/s) at 82,671-token ctx"
 PEAK_GBS = 8000.0
-REF_M4_GBS = 179892096 / 12.243627500138246e-3 / 1e9  # reference fused kernel, M4
+REF_M4_GBS = 179892096 / 12.243627500138246e-3 / 1e9  # reference fused kernel on an M4 GPU (results/kv_decode_micro_fused.json)
 HQ, HKV, D, GS = 32, 8, 128, 64
 Q8_ROW = 2 * (D + 2 * 2 * (D // GS))  # K+V codes + bf16 scale/bias per token per KV head = 272
 Q8_TOKEN = HKV * Q8_ROW               # 2176 B per token over 8 KV heads
@@ -40,12 +40,19 @@ def parse():
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--ctx", type=int, default=82671)
     p.add_argument("--layers", type=int, default=10)
-    p.add_argument("--cpu-calls", type=int, default=3, help="CPU baseline sample size (calls)")
+    p.add_argument("--event-every", type=int, default=1,
+                   help="bracket every K-th timed attention call with events (0: none, and take the "
+                        "roofline from --roofline-calls separate calls after the timed region)")
+    p.add_argument("--roofline-calls", type=int, default=64)
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="CPU baseline sample: calls are repeated until this much time has passed")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
     return p.parse_args()
 
 
-def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, calls):
+def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, seconds):
     """The reference's unfused path restated by the oracle: dequantize the cache to bf16, then
     fp32 SDPA (BLAS). The 8 KV heads run in a thread pool (NumPy releases the GIL)."""
     import numpy as np
@@ -66,10 +73,12 @@ def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, calls):
     times = []
     with ThreadPoolExecutor(threads) as ex:
         list(ex.map(one_head, range(HKV)))  # warm-up
-        for _ in range(calls):
+        t_end = time.perf_counter() + seconds
+        while len(times) < 3 or time.perf_counter() < t_end:
             t0 = time.perf_counter()
             list(ex.map(one_head, range(HKV)))
             times.append(time.perf_counter() - t0)
+    calls = len(times)
     t = sorted(times)[len(times) // 2]
     try:
         model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
@@ -84,11 +93,29 @@ def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, calls):
     }
 
 
+def copy_calibration(mib):
+    """A plain device-to-device copy of `mib` MiB, 8 times: under rocprofv3 --pmc FETCH_SIZE (or
+    WRITE_SIZE) it gives the counter's reading for a known number of HBM bytes, the factor that
+    turns the counters read on the attention kernel into bytes."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    for _ in range(8):
+        flush.fill_(0)  # evicts src/dst from the last-level cache between copies
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 8}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported on this "
-              "single-GPU build (the path would shard by KV head, see DESIGN.md)", file=sys.stderr)
+              "single-GPU build (the path would shard by KV head)", file=sys.stderr)
         sys.exit(2)
 
     import ctypes as C
@@ -97,6 +124,10 @@ def main():
     import torch
 
     from lagunalab_amd import _lib
+
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     lib = _lib.load()
     dev = torch.device("cuda", 0)
@@ -168,26 +199,42 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # ---- timed region: K steps; per-call events bracket the attention launches
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+    # ---- timed region: K steps. Every `event_every`-th step's attention call is bracketed by a
+    # pair of events on the launch stream; the roofline is taken from those calls.
+    every = args.event_every
+    evs = {j: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for j in range(args.steps) if every > 0 and j % every == 0}
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     ns = []
     torch.cuda.synchronize()
     t_start.record(stream)
     for j in range(args.steps):
-        ns.append(step(args.warmup + j, evs[j]))
+        ns.append(step(args.warmup + j, evs.get(j)))
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    attn_ms = [a.elapsed_time(b) for a, b in evs]
+    attn_ms = [a.elapsed_time(b) for a, b in evs.values()]
+    attn_n = [ns[j] for j in evs]
+    if not evs:
+        # roofline from a separate pass of event-bracketed attention calls over the same caches
+        pairs = []
+        for j in range(args.roofline_calls):
+            li = j % nl
+            e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            e[0].record(stream)
+            _lib.check(attend(j % total_steps, layers[li], offsets[li]), "roofline call")
+            e[1].record(stream)
+            pairs.append(e)
+            attn_n.append(offsets[li])
+        torch.cuda.synchronize()
+        attn_ms = [a.elapsed_time(b) for a, b in pairs]
 
     # per step: K/V codes + scales/biases over n rows, the new bf16 K/V rows read (4096 B), the
     # appended q8 K/V rows written (2176 B), q read and out written (8192 B each)
     step_bytes = [Q8_TOKEN * n + 2 * HKV * D * 2 + Q8_TOKEN + 2 * HQ * D * 2 for n in ns]
     value = sum(step_bytes) / (total_ms * 1e-3) / 1e9
-    attn_bytes = [Q8_TOKEN * n + 2 * HQ * D * 2 for n in ns]
+    attn_bytes = [Q8_TOKEN * n + 2 * HQ * D * 2 for n in attn_n]
     attn_avg_ms = sum(attn_ms) / len(attn_ms)
     attn_med_ms = sorted(attn_ms)[len(attn_ms) // 2]
     achieved = (sum(attn_bytes) / len(attn_bytes)) / (attn_avg_ms * 1e-3) / 1e9
@@ -216,17 +263,18 @@ def main():
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "lq_decode_attn (q8_decode_split_kernel + decode_merge_kernel)",
+                     "kernel": "lq_decode_attn (q8_attn_packed_kernel + decode_merge_kernel)",
+                     "calls_timed": len(attn_ms),
                      "bytes_per_call": int(sum(attn_bytes) / len(attn_bytes))},
         "vs_baseline_ref": "reference fused q8 kernel on an M4 GPU: 12.24 ms/call = 14.69 GB/s",
     }
-    if not args.no_cpu_baseline and args.cpu_calls > 0:
+    if not args.no_cpu_baseline and args.cpu_seconds > 0:
         lay = layers[0]
         n0 = offsets[0]
         host = [t[0].cpu().numpy() if t.dtype == torch.uint8 else
                 t[0].view(torch.int16).cpu().numpy().view(np.uint16) for kv in lay for t in kv]
         qn = qs[0, 0, :, 0].float().cpu().numpy()
-        res["cpu_baseline"] = cpu_baseline(*host, qn, n0, args.cpu_calls)
+        res["cpu_baseline"] = cpu_baseline(*host, qn, n0, args.cpu_seconds)
         res["cpu_baseline"]["value_vs_gpu"] = round(value / res["cpu_baseline"]["value"], 1)
     print(json.dumps(res), flush=True)
 

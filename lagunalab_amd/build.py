@@ -28,6 +28,9 @@ FLAGS = [
     "-Wno-unused-function",
     # never emit packed fp32 VALU ops (v_pk_fma_f32 and friends)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the attention loops rescale their output accumulators on the
+    # VALU, which with AGPR accumulators costs a copy of every accumulator per key tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -92,6 +92,24 @@ __device__ __forceinline__ void g2l_b128(const void* g, void* lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :: "v"(g), "s"(lds_u32(lds_base)) : "memory");
 }
+// Same copies with a wave-uniform global base (SGPR pair) plus a 32-bit per-lane offset, into
+// LDS at lds + LOFF (lds wave-uniform): no 64-bit address arithmetic per lane and no
+// readfirstlane per copy. The instruction's immediate offset stays 0 (it would move the LDS
+// destination too). The asm only moves into M0 (no SCC-writing instruction: the compiler may
+// keep a carry live across the statement).
+template <int LOFF>
+__device__ __forceinline__ void dma_b128(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
+}
+template <int LOFF>
+__device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
 
 template <int NT, bool CAUSAL>
 __global__ __launch_bounds__(NTHR) void q8_attn_mfma_kernel(
@@ -449,7 +467,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
   const int x = blockIdx.x;
   const int hk = blockIdx.y;
   int b;
@@ -511,24 +529,62 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const int causal_bound = n - L + qi;  // query qi sees keys t <= causal_bound
   PackTerms& tm = sm.loop.terms[wv];
 
-  // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays
+  // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
+  // bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the LDS row (the
+  // swizzle read back in process). A full super-tile uses the scalar row base t0 and per-lane
+  // offsets that never change; the last one clamps rows to the wave's last key (past the end the
+  // copies land in the unused buffer and are never read).
+  const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
+  const uint32_t col_off = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
+  uint32_t row_off[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
   auto issue = [&](int si) {
     const int t0 = w_begin + si * PST;
-    const int last = max(w_end - 1, 0);
-    PackBuf& pb = sm.loop.buf[wv][si & 1];
+    const uint32_t lb = lds_bufs + (uint32_t)(si & 1) * (uint32_t)sizeof(PackBuf);
+    constexpr int OK = offsetof(PackBuf, k), OV = offsetof(PackBuf, v);
+    constexpr int OKS = offsetof(PackBuf, ks), OKB = offsetof(PackBuf, kb);
+    constexpr int OVS = offsetof(PackBuf, vs), OVB = offsetof(PackBuf, vb);
+    const uint8_t* kb0 = kbase;
+    const uint8_t* vb0 = vbase;
+    const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
+    uint32_t ro[8], wo;
+    if (t0 + PST <= w_end) {
+      kb0 += (int64_t)t0 * D;
+      vb0 += (int64_t)t0 * D;
+      w0 += t0;
+      w1 += t0;
+      w2 += t0;
+      w3 += t0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int row = (lane >> 3) + 8 * u;
-      const int64_t t = min(t0 + row, last);
-      const int chunk = (lane & 7) ^ (row & 7);
-      g2l_b128(kbase + t * D + 16 * chunk, pb.k + 1024 * u);
-      g2l_b128(vbase + t * D + 16 * chunk, pb.v + 1024 * u);
+      for (int u = 0; u < 8; ++u) ro[u] = row_off[u];
+      wo = 4u * (uint32_t)lane;
+    } else {
+      const int last = max(w_end - 1, 0);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last) * D + col_off;
+      wo = 4u * (uint32_t)min(t0 + lane, last);
     }
-    const int64_t ts = min(t0 + lane, last);
-    g2l_b32(ksw + ts, pb.ks);
-    g2l_b32(kbw + ts, pb.kb);
-    g2l_b32(vsw + ts, pb.vs);
-    g2l_b32(vbw + ts, pb.vb);
+    dma_b128<OK + 0>(kb0, ro[0], lb);
+    dma_b128<OV + 0>(vb0, ro[0], lb);
+    dma_b128<OK + 1024>(kb0, ro[1], lb);
+    dma_b128<OV + 1024>(vb0, ro[1], lb);
+    dma_b128<OK + 2048>(kb0, ro[2], lb);
+    dma_b128<OV + 2048>(vb0, ro[2], lb);
+    dma_b128<OK + 3072>(kb0, ro[3], lb);
+    dma_b128<OV + 3072>(vb0, ro[3], lb);
+    dma_b128<OK + 4096>(kb0, ro[4], lb);
+    dma_b128<OV + 4096>(vb0, ro[4], lb);
+    dma_b128<OK + 5120>(kb0, ro[5], lb);
+    dma_b128<OV + 5120>(vb0, ro[5], lb);
+    dma_b128<OK + 6144>(kb0, ro[6], lb);
+    dma_b128<OV + 6144>(vb0, ro[6], lb);
+    dma_b128<OK + 7168>(kb0, ro[7], lb);
+    dma_b128<OV + 7168>(vb0, ro[7], lb);
+    dma_b32<OKS>(w0, wo, lb);
+    dma_b32<OKB>(w1, wo, lb);
+    dma_b32<OVS>(w2, wo, lb);
+    dma_b32<OVB>(w3, wo, lb);
   };
 
   auto process = [&](int si) {
@@ -548,23 +604,20 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       tm.vb0[lane] = bf16_to_f32((uint16_t)(f & 0xffffu));
       tm.vb1[lane] = bf16_to_f32((uint16_t)(f >> 16));
     }
-    // Q.K^T: A = key row lc of tile lq4, 16 steps of 8 dims (two steps per 16-byte LDS read)
+    // Q.K^T: A = key row lc of tile lq4, 16 steps of 8 dims (two steps per 16-byte LDS read);
+    // the two quant groups accumulate in independent chains, interleaved.
     f4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
     {
       const int r = 16 * lq4 + lc;
       const uint8_t* kr = pb.k + r * D;
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) {
+      for (int s2 = 0; s2 < 4; ++s2) {
         const uint4 a = *reinterpret_cast<const uint4*>(kr + 16 * (s2 ^ (r & 7)));
-        const half8_t a0 = codes8_as_h8(a.x, a.y);
-        const half8_t a1 = codes8_as_h8(a.z, a.w);
-        if (s2 < 4) {
-          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qb[2 * s2], c0, 0, 0, 0);
-          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qb[2 * s2 + 1], c0, 0, 0, 0);
-        } else {
-          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qb[2 * s2], c1, 0, 0, 0);
-          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qb[2 * s2 + 1], c1, 0, 0, 0);
-        }
+        const uint4 b = *reinterpret_cast<const uint4*>(kr + 16 * ((s2 + 4) ^ (r & 7)));
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(a.x, a.y), qb[2 * s2], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(b.x, b.y), qb[2 * s2 + 8], c1, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(a.z, a.w), qb[2 * s2 + 1], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(b.z, b.w), qb[2 * s2 + 9], c1, 0, 0, 0);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -596,8 +649,8 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     // max over the 4 key tiles (lanes 4 apart in a row) and the 4 lane groups
     tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
     tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;
     if (__builtin_amdgcn_ballot_w64(bump)) {
       const float mn = bump ? tmax : m_run;
@@ -680,8 +733,8 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     float v = tot[k];
     v += dpp<DPP_ROW_ROR4>(v);
     v += dpp<DPP_ROW_ROR8>(v);
-    v += shfl_xor_f(v, 16);
-    v += shfl_xor_f(v, 32);
+    v = sum_xor16(v);
+    v = sum_xor32(v);
     tot[k] = v;
   }
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below

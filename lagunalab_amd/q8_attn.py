@@ -8,7 +8,7 @@ query, a head_dim other than 128, a cache that is not 8-bit, or too many query h
 ``q8_attn.py:110-115``). Codes may be given as uint8 ``[..., D]`` or as MLX-style 32-bit words
 ``[..., D // 4]`` (int32/uint32; byte-identical on little-endian hosts).
 
-Additions behind the same layout (the north-star extensions): ragged batches with per-sequence
+Additions behind the same layout: ragged batches with per-sequence
 lengths (:func:`decode_attention` with ``lens``), the multi-query causal verify step
 (:func:`q8_verify_attention`), and 4-bit / plain-bf16 caches (:func:`decode_attention` with
 ``kind``).

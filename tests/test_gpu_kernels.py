@@ -4,7 +4,7 @@ the C ABI. Bit-exact for codes, scales, biases, dequantized values, draft ids an
 Attention is checked twice: (1) against the fused-kernel arithmetic (fp32 dequantize, as the
 reference's Metal kernel does, q8_attn.py:46-55) within max-abs 2e-3 + rel 1e-2 at every size;
 (2) against the reference's unfused path (dequantize to bf16, then SDPA) within the same
-2e-3 + 1e-2 from 4,096 keys up (the north-star configurations), and within the reference's own
+2e-3 + 1e-2 from 4,096 keys up (the benchmarked context lengths), and within the reference's own
 fused-vs-unfused tolerance of 2e-2 (tests/test_q8_attn.py:31) below that, where the bf16 rounding
 of a handful of V rows is not averaged away."""
 import numpy as np
