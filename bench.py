@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--ctx", type=int, default=82671)
     p.add_argument("--layers", type=int, default=10)
-    p.add_argument("--event-every", type=int, default=1,
+    p.add_argument("--event-every", type=int, default=8,
                    help="bracket every K-th timed attention call with events (0: none, and take the "
                         "roofline from --roofline-calls separate calls after the timed region)")
     p.add_argument("--roofline-calls", type=int, default=64)
@@ -162,7 +162,7 @@ def main():
     vs_new = torch.randn((total_steps, 1, HKV, 1, D), device=dev, generator=g).to(torch.bfloat16)
     out = torch.empty((1, HQ, 1, D), dtype=torch.bfloat16, device=dev)
     ws_bytes = lib.lq_decode_workspace_bytes(8, 1, HQ, HKV, D, ctx + grow, None)
-    ws = torch.empty(ws_bytes * 2, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes * 2, dtype=torch.uint8, device=dev)  # leading counters start at 0
     offsets = [ctx] * nl
     torch.cuda.synchronize()
 
@@ -263,7 +263,7 @@ def main():
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "lq_decode_attn (q8_attn_packed_kernel + decode_merge_kernel)",
+                     "kernel": "lq_decode_attn (q8_attn_packed_kernel, split merge fused)",
                      "calls_timed": len(attn_ms),
                      "bytes_per_call": int(sum(attn_bytes) / len(attn_bytes))},
         "vs_baseline_ref": "reference fused q8 kernel on an M4 GPU: 12.24 ms/call = 14.69 GB/s",

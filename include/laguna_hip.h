@@ -34,6 +34,14 @@ extern "C" {
 
 #define LQ_MAX_SEQS 64  /* sequences per ragged decode call */
 
+/*
+ * Attention workspaces (lq_decode_attn, lq_q8_verify_attn) start with LQ_WS_ZERO_BYTES bytes of
+ * arrival counters that must be zero before the first call that uses the workspace (clear them
+ * once after allocating it); every call leaves them zero again. Calls that share a workspace
+ * must be ordered (one stream). At most LQ_WS_ZERO_BYTES / 4 (sequence, KV head) pairs per call.
+ */
+#define LQ_WS_ZERO_BYTES 16384
+
 /* Library version (major*10000 + minor*100 + patch). */
 int lq_version(void);
 
@@ -74,7 +82,7 @@ int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, 
  * Fused single-token decode attention. Replaces q8_decode_attention(q, keys, values, n, scale)
  * (laguna_mlx/q8_attn.py:102-130: the Metal kernel N1 at :17-99 and the block merge at
  * :126-130) and generalises it to 4-bit and plain-bf16 caches and to ragged batches.
- *   q    bf16 [B, Hq, 1, D] contiguous, D == 128, Hq % Hkv == 0, Hq / Hkv <= 8
+ *   q    bf16 [B, Hq, 1, D] contiguous, D == 128, Hq % Hkv == 0, Hq / Hkv <= 16
  *   kc..vb the cache buffers of one layer (layout above; for LQ_KV_BF16, kc and vc are bf16
  *          [B, Hkv, cap, D])
  *   n    valid rows when lens_host == NULL; otherwise lens_host[b] (host array, B <= 64,

@@ -77,6 +77,16 @@ __device__ __forceinline__ half2_t codes_as_h2(uint32_t w, uint32_t sel) {
 constexpr uint32_t SEL_B01 = 0x04010400u;
 constexpr uint32_t SEL_B23 = 0x04030402u;
 
+// Two codes of w as fp16 subnormals (bit pattern 0x00cc = c * 2^-24, exact): bytes (0,1) or (2,3).
+__device__ __forceinline__ uint32_t codes_sub_w(uint32_t w, uint32_t sel) {
+  return __builtin_amdgcn_perm(0u, w, sel);
+}
+constexpr uint32_t SUB_B01 = 0x0c010c00u;
+constexpr uint32_t SUB_B23 = 0x0c030c02u;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
   return __builtin_amdgcn_fdot2(a, b, c, false);
 }

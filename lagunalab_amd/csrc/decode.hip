@@ -133,16 +133,19 @@ void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq
       part_acc, part_ml, rows_per_seq, plan, out);
 }
 
+bool attn_merges_itself(int64_t rows_per_kv_head) { return rows_per_kv_head <= 4; }
+
 // Shared by decode (L = 1) and verify (L <= 16): plan + workspace size for the MFMA kernel.
 int64_t attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n, const int32_t* lens,
                   int64_t cap, DecodePlan& plan, QAttnFn& fn, int64_t& ws_bytes) {
   const int64_t R = (Hq / Hkv) * L;
-  const int nt = R <= 4 ? 0 : (int)((R + 15) / 16);  // 0: the packed kernel
+  const int nt = attn_merges_itself(R) ? 0 : (int)((R + 15) / 16);  // 0: the packed kernel
   fn = q8_attn_fn(nt, L > 1);
   if (!fn) return -1;
+  if (B * Hkv > MAX_COUNTERS) return -1;
   const int64_t S = make_plan(B, Hkv, n, lens, cap, attn_occupancy(fn) * device_cu_count(), plan);
   if (S < 0) return -1;
-  ws_bytes = S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
+  ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
   return S;
 }
 
@@ -181,7 +184,9 @@ extern "C" int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const
   LQ_CHECK_ARG(Hq / Hkv <= 16, "at most 16 query heads per KV head (got %lld)",
                (long long)(Hq / Hkv));
   LQ_CHECK_ARG(B >= 1 && B <= LQ_MAX_SEQS, "batch %lld outside [1, %d]", (long long)B, LQ_MAX_SEQS);
-  LQ_CHECK_ARG(cap >= 1 && cap <= INT32_MAX, "bad capacity %lld", (long long)cap);
+  LQ_CHECK_ARG(cap >= 1 && cap <= (1 << 24), "capacity %lld outside [1, 2^24]", (long long)cap);
+  LQ_CHECK_ARG(B * Hkv <= MAX_COUNTERS, "B * Hkv = %lld exceeds %lld", (long long)(B * Hkv),
+               (long long)MAX_COUNTERS);
   LQ_CHECK_ARG(q && kc && ks && kb && vc && vs && vb && out, "null pointer");
   DecodePlan plan;
   QAttnFn fn;
@@ -193,15 +198,18 @@ extern "C" int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  float* part_acc = reinterpret_cast<float*>(workspace);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
+  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
   float2* part_ml = reinterpret_cast<float2*>(part_acc + S * Hq * D);
   hipStream_t st = (hipStream_t)stream;
   const float qk = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, q,
                      (const uint8_t*)kc, ks, kb, (const uint8_t*)vc, vs, vb, (int)Hkv,
-                     (int)(Hq / Hkv), 1, cap, qk, plan, part_acc, part_ml);
-  LQ_CHECK_LAUNCH("q8_attn_mfma_kernel");
-  launch_merge(part_acc, part_ml, (int)Hq, plan, B, out, st);
-  LQ_CHECK_LAUNCH("decode_merge_kernel");
+                     (int)(Hq / Hkv), 1, cap, qk, plan, part_acc, part_ml, counters, out);
+  LQ_CHECK_LAUNCH("q8 attention kernel");
+  if (!attn_merges_itself(Hq / Hkv)) {
+    launch_merge(part_acc, part_ml, (int)Hq, plan, B, out, st);
+    LQ_CHECK_LAUNCH("decode_merge_kernel");
+  }
   return LQ_OK;
 }

@@ -27,16 +27,27 @@ __device__ __forceinline__ void find_seq(const DecodePlan& plan, int x, int& b) 
 
 typedef void (*QAttnFn)(const uint16_t*, const uint8_t*, const uint16_t*, const uint16_t*,
                         const uint8_t*, const uint16_t*, const uint16_t*, int, int, int, int64_t,
-                        float, DecodePlan, float*, float2*);
+                        float, DecodePlan, float*, float2*, uint32_t*, uint16_t*);
+
+// Workspace of the attention calls: arrival counters (one per sequence and KV head, zero
+// between calls: each call's last arrival resets its counter) at the start, then the split
+// partials. The counter area has a fixed size so that calls of any shape can share a workspace.
+constexpr int64_t WS_COUNTER_BYTES = LQ_WS_ZERO_BYTES;
+constexpr int64_t MAX_COUNTERS = WS_COUNTER_BYTES / 4;
 
 // MFMA attention kernel for `nt` 16-column tiles of query rows (G * L <= 16 * nt), causal for
-// multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4.
+// multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4, which also merges
+// the splits (no decode_merge_kernel launch).
 QAttnFn q8_attn_fn(int nt, bool causal);
 
 // Plan + workspace bytes for an attention call with L query rows per head; returns the number
 // of splits (or -1) and selects the kernel.
 int64_t attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n, const int32_t* lens,
                   int64_t cap, DecodePlan& plan, QAttnFn& fn, int64_t& ws_bytes);
+
+// True when the attention kernel for this many query rows per KV head (G * L) merges the
+// split partials itself (the packed kernel).
+bool attn_merges_itself(int64_t rows_per_kv_head);
 
 // Per-sequence log-sum-exp merge of split partials: rows_per_seq = Hq * L partial rows per split.
 void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq,

@@ -23,8 +23,11 @@
 //    ds_read_b64_tr_b8 (one 8-byte transposed read per operand) and B = P * scale_v in fp16.
 //    The keys of B's k-slots are ordered exactly as the lane already holds them after Q.K^T,
 //    so P never leaves registers. Bias and 1024-offset terms are per-row sums, not per element.
-//  * Partials (m, l, acc[128]) per (split, query row) go to the workspace; decode_merge_kernel
-//    does the per-sequence log-sum-exp merge.
+//  * Partials (m, l, acc[128]) per (split, query row) go to the workspace. The packed kernel
+//    merges them itself (the last workgroup of each sequence and KV head to finish, counted with
+//    one atomic per workgroup); after the general kernel decode_merge_kernel does the merge.
+#include <type_traits>
+
 #include "common.h"
 #include "qattn.h"
 
@@ -73,6 +76,24 @@ __device__ __forceinline__ half8_t codes8_as_h8(uint32_t w0, uint32_t w1) {
   return r;
 }
 
+// 8 codes (two words) as fp16 subnormals c * 2^-24 for an MFMA operand.
+__device__ __forceinline__ half8_t codes8_sub(uint32_t w0, uint32_t w1) {
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t u = {codes_sub_w(w0, SUB_B01), codes_sub_w(w0, SUB_B23), codes_sub_w(w1, SUB_B01),
+                   codes_sub_w(w1, SUB_B23)};
+  return __builtin_bit_cast(half8_t, u);
+}
+__device__ __forceinline__ half8_t words_as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t u = {a, b, c, d};
+  return __builtin_bit_cast(half8_t, u);
+}
+// Two floats as one dword of fp16 (round to nearest even), x in the low half.
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  const half2_t h = {(_Float16)x, (_Float16)y};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
 
 // Global -> LDS copies (LDS destination = lds_base + size * lane; lds_base wave-uniform). They are
@@ -117,7 +138,8 @@ __global__ __launch_bounds__(NTHR) void q8_attn_mfma_kernel(
     const uint16_t* __restrict__ ks, const uint16_t* __restrict__ kb,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vs,
     const uint16_t* __restrict__ vb, int Hkv, int G, int L, int64_t cap, float qk_scale_log2,
-    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml) {
+    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml,
+    uint32_t* __restrict__ /*counters*/, uint16_t* __restrict__ /*out*/) {
   __shared__ QSmem<NT> sm;
 
   const int tid = threadIdx.x;
@@ -456,14 +478,107 @@ struct PackSmem {
   float st[NWAVE][4][6];
 };
 
+// Agent-scope relaxed atomic accesses: written through to / read from the device-coherent level,
+// so partials published by one workgroup are visible to a workgroup on another XCD without
+// writing back or invalidating a whole L2 (which a fence would do in every workgroup).
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Log-sum-exp merge of the split partials of sequence b, KV head hk (R <= 4 query rows) by one
+// workgroup, into the output rows (b * Hkv + hk) * R + row of out [B, Hq, L, D] (bf16).
+// Partial (m, l, acc) of split s, row r: part_ml / part_acc at (s * Hkv + hk) * R + r.
+// Thread t takes 4 dims (t % 32) of row (t % 128) / 32 over the splits of parity t / 128: it
+// loads (m, l, acc) of up to MCH splits at once (one memory round trip for up to 2 MCH splits),
+// merges them with its own running max, and the two parities meet in LDS. red: LDS scratch of
+// at least 768 floats.
+constexpr int MCH = 16;
+__device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& plan,
+                            const float* __restrict__ part_acc,
+                            const float2* __restrict__ part_ml, uint16_t* __restrict__ out,
+                            float* red) {
+  const int tid = threadIdx.x;
+  const int s0 = plan.split_begin[b];
+  const int ns = plan.split_begin[b + 1] - s0;
+  const int64_t rs = (int64_t)Hkv * R;
+  const int64_t r0 = (int64_t)hk * R;
+  const float* pml = reinterpret_cast<const float*>(part_ml);
+  const int o = tid & 127;
+  const int row = o >> 5;
+  const int d0 = 4 * (o & 31);
+  const int par = tid >> 7;
+  float M = -INFINITY, den = 0.0f;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if (row < R) {
+    for (int base = par; base < ns; base += 2 * MCH) {
+      float mv[MCH], lv[MCH], av[MCH][4];
+#pragma unroll
+      for (int k = 0; k < MCH; ++k) {
+        const int sk = min(base + 2 * k, ns - 1);
+        const int64_t pr = (s0 + sk) * rs + r0 + row;
+        mv[k] = ld_agent(pml + 2 * pr);
+        lv[k] = ld_agent(pml + 2 * pr + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) av[k][j] = ld_agent(part_acc + pr * D + d0 + j);
+      }
+      float cm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < MCH; ++k)
+        if (base + 2 * k < ns) cm = fmaxf(cm, mv[k]);
+      const float Mn = fmaxf(M, cm);
+      if (Mn != -INFINITY) {
+        const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+        den *= sc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] *= sc;
+#pragma unroll
+        for (int k = 0; k < MCH; ++k) {
+          const float w = (base + 2 * k < ns && mv[k] != -INFINITY) ? exp2f(mv[k] - Mn) : 0.0f;
+          den += w * lv[k];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[j] += w * av[k][j];
+        }
+        M = Mn;
+      }
+    }
+  }
+  // parity 1 hands (M, den, a) to parity 0 through LDS
+  if (par == 1) {
+    red[o] = M;
+    red[128 + o] = den;
+    *reinterpret_cast<float4*>(red + 256 + 4 * o) = make_float4(a[0], a[1], a[2], a[3]);
+  }
+  __syncthreads();
+  if (par == 0 && row < R) {
+    const float M1 = red[o], den1 = red[128 + o];
+    const float4 a1 = *reinterpret_cast<const float4*>(red + 256 + 4 * o);
+    const float Mx = fmaxf(M, M1);
+    const float e0 = M == -INFINITY ? 0.0f : exp2f(M - Mx);
+    const float e1 = M1 == -INFINITY ? 0.0f : exp2f(M1 - Mx);
+    const float inv = 1.0f / (e0 * den + e1 * den1);
+    const float r0v = (e0 * a[0] + e1 * a1.x) * inv, r1v = (e0 * a[1] + e1 * a1.y) * inv;
+    const float r2v = (e0 * a[2] + e1 * a1.z) * inv, r3v = (e0 * a[3] + e1 * a1.w) * inv;
+    const uint32_t lo = (uint32_t)f32_to_bf16(r0v) | ((uint32_t)f32_to_bf16(r1v) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(r2v) | ((uint32_t)f32_to_bf16(r3v) << 16);
+    *reinterpret_cast<uint2*>(out + (((int64_t)b * Hkv + hk) * R + row) * D + d0) = make_uint2(lo, hi);
+  }
+}
+
 template <bool CAUSAL>
 __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ ks, const uint16_t* __restrict__ kb,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vs,
     const uint16_t* __restrict__ vb, int Hkv, int G, int L, int64_t cap, float qk_scale_log2,
-    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml) {
+    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml,
+    uint32_t* __restrict__ counters, uint16_t* __restrict__ out) {
   __shared__ PackSmem sm;
+  __shared__ int sh_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -491,32 +606,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const int gh = qvalid ? rho / L : 0;
   const int qi = qvalid ? rho - gh * L : 0;
 
-  // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
-  half8_t qb[16];
+  half8_t qb[16];  // Q.K^T B operands (filled once the first super-tile is in flight)
   float qsum[2];
-  {
-    const bool on = qvalid && mt == lq4;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
-    float sg[2] = {0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * st);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const _Float16 lo = (_Float16)bf16_to_f32((uint16_t)(w[j] & 0xffffu));
-        const _Float16 hi = (_Float16)bf16_to_f32((uint16_t)(w[j] >> 16));
-        qb[st][2 * j] = on ? lo : (_Float16)0.0f;
-        qb[st][2 * j + 1] = on ? hi : (_Float16)0.0f;
-        sg[st >> 3] += (float)lo + (float)hi;
-      }
-    }
-    qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
-    qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
-  }
-
   f4_t oacc[8];
-  float m_run = -INFINITY, lsum = 0.f, wsum0 = 0.f, wsum1 = 0.f, bsum0 = 0.f, bsum1 = 0.f;
+  float m_run = -INFINITY, lsum = 0.f, bsum0 = 0.f, bsum1 = 0.f;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) oacc[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -539,9 +632,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   uint32_t row_off[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
-  auto issue = [&](int si) {
+  auto issue = [&](int si, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
     const int t0 = w_begin + si * PST;
-    const uint32_t lb = lds_bufs + (uint32_t)(si & 1) * (uint32_t)sizeof(PackBuf);
+    const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(PackBuf));
     constexpr int OK = offsetof(PackBuf, k), OV = offsetof(PackBuf, v);
     constexpr int OKS = offsetof(PackBuf, ks), OKB = offsetof(PackBuf, kb);
     constexpr int OVS = offsetof(PackBuf, vs), OVB = offsetof(PackBuf, vb);
@@ -587,25 +681,30 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     dma_b32<OVB>(w3, wo, lb);
   };
 
-  auto process = [&](int si) {
+  // Lane masks selecting the P.V B-operand half of K-step e (key tile 2e in slots 0-3, 2e+1 in
+  // slots 4-7): this lane's own key tile is mt.
+  const uint32_t sel_lo0 = mt == 0 ? ~0u : 0u, sel_hi0 = mt == 1 ? ~0u : 0u;
+  const uint32_t sel_lo1 = mt == 2 ? ~0u : 0u, sel_hi1 = mt == 3 ? ~0u : 0u;
+  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+
+  auto process = [&](int si, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
     const int t0 = w_begin + si * PST;
-    const PackBuf& pb = sm.loop.buf[wv][si & 1];
-    // per-key terms, one lane per key
+    const PackBuf& pb = sm.loop.buf[wv][BUF];
+    // per-key terms, one lane per key: K scale * scale * log2(e) * 2^24, K bias, V scale, V bias
     {
       const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
-      const float s0 = bf16_to_f32((uint16_t)(a & 0xffffu)), s1 = bf16_to_f32((uint16_t)(a >> 16));
-      const float b0 = bf16_to_f32((uint16_t)(c & 0xffffu)), b1 = bf16_to_f32((uint16_t)(c >> 16));
-      tm.ks0[lane] = s0 * qk_scale_log2;
-      tm.ks1[lane] = s1 * qk_scale_log2;
-      tm.ku0[lane] = b0 - 1024.0f * s0;
-      tm.ku1[lane] = b1 - 1024.0f * s1;
-      tm.vs0[lane] = bf16_to_f32((uint16_t)(e & 0xffffu));
-      tm.vs1[lane] = bf16_to_f32((uint16_t)(e >> 16));
-      tm.vb0[lane] = bf16_to_f32((uint16_t)(f & 0xffffu));
-      tm.vb1[lane] = bf16_to_f32((uint16_t)(f >> 16));
+      tm.ks0[lane] = bf16_lo(a) * kscale;
+      tm.ks1[lane] = bf16_hi(a) * kscale;
+      tm.ku0[lane] = bf16_lo(c);
+      tm.ku1[lane] = bf16_hi(c);
+      tm.vs0[lane] = bf16_lo(e);
+      tm.vs1[lane] = bf16_hi(e);
+      tm.vb0[lane] = bf16_lo(f);
+      tm.vb1[lane] = bf16_hi(f);
     }
-    // Q.K^T: A = key row lc of tile lq4, 16 steps of 8 dims (two steps per 16-byte LDS read);
-    // the two quant groups accumulate in independent chains, interleaved.
+    // Q.K^T: A = key row lc of tile lq4 (codes as fp16 subnormals c * 2^-24), 16 steps of 8 dims
+    // (two steps per 16-byte LDS read); the two quant groups accumulate in independent chains.
     f4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
     {
       const int r = 16 * lq4 + lc;
@@ -614,10 +713,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       for (int s2 = 0; s2 < 4; ++s2) {
         const uint4 a = *reinterpret_cast<const uint4*>(kr + 16 * (s2 ^ (r & 7)));
         const uint4 b = *reinterpret_cast<const uint4*>(kr + 16 * ((s2 + 4) ^ (r & 7)));
-        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(a.x, a.y), qb[2 * s2], c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(b.x, b.y), qb[2 * s2 + 8], c1, 0, 0, 0);
-        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(a.z, a.w), qb[2 * s2 + 1], c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_as_h8(b.z, b.w), qb[2 * s2 + 9], c1, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_sub(a.x, a.y), qb[2 * s2], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_sub(b.x, b.y), qb[2 * s2 + 8], c1, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_sub(a.z, a.w), qb[2 * s2 + 1], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_sub(b.z, b.w), qb[2 * s2 + 9], c1, 0, 0, 0);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -636,7 +735,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const bool full = t0 + PST <= w_end && (!CAUSAL || t0 + PST - 1 <= n - L);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float v = ks0v[r] * c0[r] + ks1v[r] * c1[r] + (ku0v[r] * qsum[0] + ku1v[r] * qsum[1]);
+      float v = fmaf(ks0v[r], c0[r], fmaf(ks1v[r], c1[r], fmaf(ku1v[r], qsum[1], ku0v[r] * qsum[0])));
       if (!full) {
         const int t = t0 + k0 + r;
         bool ok = t < w_end;
@@ -657,8 +756,6 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       const float alpha = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
       m_run = mn;
       lsum *= alpha;
-      wsum0 *= alpha;
-      wsum1 *= alpha;
       bsum0 *= alpha;
       bsum1 *= alpha;
 #pragma unroll
@@ -671,30 +768,25 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const float4 vb1 = *reinterpret_cast<const float4*>(tm.vb1 + k0);
     const float vs0v[4] = {vs0.x, vs0.y, vs0.z, vs0.w}, vs1v[4] = {vs1.x, vs1.y, vs1.z, vs1.w};
     const float vb0v[4] = {vb0.x, vb0.y, vb0.z, vb0.w}, vb1v[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
-    _Float16 w0[4], w1[4];
+    float p[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float p = __builtin_amdgcn_exp2f(sc[r] - mref);
-      w0[r] = (_Float16)(p * vs0v[r]);
-      w1[r] = (_Float16)(p * vs1v[r]);
-      lsum += p;
-      wsum0 += (float)w0[r];
-      wsum1 += (float)w1[r];
-      bsum0 += p * vb0v[r];
-      bsum1 += p * vb1v[r];
+      p[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
+      lsum += p[r];
+      bsum0 = fmaf(p[r], vb0v[r], bsum0);
+      bsum1 = fmaf(p[r], vb1v[r], bsum1);
     }
+    // P * scale_v in fp16, two keys per dword, per quant group
+    const uint32_t w00 = pack_h2(p[0] * vs0v[0], p[1] * vs0v[1]);
+    const uint32_t w01 = pack_h2(p[2] * vs0v[2], p[3] * vs0v[3]);
+    const uint32_t w10 = pack_h2(p[0] * vs1v[0], p[1] * vs1v[1]);
+    const uint32_t w11 = pack_h2(p[2] * vs1v[2], p[3] * vs1v[3]);
     // P.V, K-step e covers key tiles 2e (slots 0-3) and 2e+1 (slots 4-7)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      half8_t b0, b1;
-      const bool lo = mt == 2 * e, hi = mt == 2 * e + 1;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        b0[r] = lo ? w0[r] : (_Float16)0.0f;
-        b0[4 + r] = hi ? w0[r] : (_Float16)0.0f;
-        b1[r] = lo ? w1[r] : (_Float16)0.0f;
-        b1[4 + r] = hi ? w1[r] : (_Float16)0.0f;
-      }
+      const uint32_t slo = e == 0 ? sel_lo0 : sel_lo1, shi = e == 0 ? sel_hi0 : sel_hi1;
+      const half8_t b0 = words_as_h8(w00 & slo, w01 & slo, w00 & shi, w01 & shi);
+      const half8_t b1 = words_as_h8(w10 & slo, w11 & slo, w10 & shi, w11 & shi);
       const int j = lc >> 1;
       const int key = 16 * (2 * e + (j >> 2)) + 4 * lq4 + (j & 3);
       const uint8_t* vrow = pb.v + key * D + 8 * (lc & 1);
@@ -702,18 +794,52 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const v2i_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (dt ^ sw)));
-        const half8_t a = codes8_as_h8((uint32_t)raw.x, (uint32_t)raw.y);
+        const half8_t a = codes8_sub((uint32_t)raw.x, (uint32_t)raw.y);
         oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, dt < 4 ? b0 : b1, oacc[dt], 0, 0, 0);
       }
     }
   };
 
-  issue(0);
-  for (int si = 0; si < nst; ++si) {
+  const std::integral_constant<int, 0> B0;
+  const std::integral_constant<int, 1> B1;
+  issue(0, B0);  // the first super-tile streams in while q is loaded and converted
+
+  // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
+  {
+    const bool on = qvalid && mt == lq4;
+    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
+    float sg[2] = {0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * st);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const _Float16 lo = (_Float16)bf16_to_f32((uint16_t)(w[j] & 0xffffu));
+        const _Float16 hi = (_Float16)bf16_to_f32((uint16_t)(w[j] >> 16));
+        qb[st][2 * j] = on ? lo : (_Float16)0.0f;
+        qb[st][2 * j + 1] = on ? hi : (_Float16)0.0f;
+        sg[st >> 3] += (float)lo + (float)hi;
+      }
+    }
+    qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
+    qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
+  }
+
+  // Unrolled by two so that each buffer's LDS offsets are constants. Super-tile si + 1 is always
+  // issued before si is processed (past the last super-tile the copies clamp to the wave's last
+  // row and are never read), so the wait is a fixed count: the 20 copies issued after si's.
+  for (int si = 0; si < nst; si += 2) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
-    issue(si + 1);
+    issue(si + 1, B1);
     asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile si has landed in LDS
-    process(si);
+    process(si, B0);
+    if (si + 1 < nst) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(si + 2, B0);
+      asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+      process(si + 1, B1);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -727,9 +853,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       v += dpp<DPP_ROW_ROR8>(v);
       oacc[dt][r] = v;
     }
-  float tot[5] = {lsum, wsum0, wsum1, bsum0, bsum1};
+  float tot[3] = {lsum, bsum0, bsum1};
 #pragma unroll
-  for (int k = 0; k < 5; ++k) {
+  for (int k = 0; k < 3; ++k) {
     float v = tot[k];
     v += dpp<DPP_ROW_ROR4>(v);
     v += dpp<DPP_ROW_ROR8>(v);
@@ -749,8 +875,6 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       st[1] = tot[0];
       st[2] = tot[1];
       st[3] = tot[2];
-      st[4] = tot[3];
-      st[5] = tot[4];
     }
   }
   __syncthreads();
@@ -766,9 +890,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     for (int w = 0; w < NWAVE; ++w) {
       const float* st = sm.st[w][col];
       const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
-      a += e * ((sm.acc[w][col][d] - 1024.0f * st[2 + g]) + st[4 + g]);
+      a += e * fmaf(sm.acc[w][col][d], 16777216.0f, st[2 + g]);
     }
-    part_acc[((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d] = a;
+    st_agent(part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
   }
   if (tid < R) {
     const int col = tid;
@@ -781,8 +905,29 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       const float* st = sm.st[w][col];
       l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
     }
-    part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
+    float* pml = reinterpret_cast<float*>(part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col);
+    st_agent(pml, M);
+    st_agent(pml + 1, l);
   }
+
+  // ---- split merge, fused: the last workgroup of (sequence, KV head) to store its partials
+  // merges those of all the sequence's splits and writes the output rows. The partials are
+  // written and read with agent-scope atomics; every thread's stores have completed (vmcnt 0)
+  // before the barrier that precedes the arrival count, and the last workgroup reads only after
+  // its count returned. The last arrival also resets the counter to zero for the next call.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* c = counters + b * Hkv + hk;
+    const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
+    const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev + 1 == ns;
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = last;
+  }
+  __syncthreads();
+  if (!sh_last) return;
+  merge_rows4(b, hk, Hkv, R, plan, part_acc, part_ml, out, &sm.acc[0][0][0]);
 }
 
 }  // namespace

@@ -41,8 +41,10 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
   LQ_CHECK_ARG((Hq / Hkv) * L <= 64, "G * L = %lld query rows per KV head exceed 64",
                (long long)((Hq / Hkv) * L));
   LQ_CHECK_ARG(B >= 1 && B <= LQ_MAX_SEQS, "batch %lld outside [1, %d]", (long long)B, LQ_MAX_SEQS);
-  LQ_CHECK_ARG(n >= L && n <= cap && cap <= INT32_MAX, "n=%lld must be in [L, cap=%lld]",
+  LQ_CHECK_ARG(n >= L && n <= cap && cap <= (1 << 24), "n=%lld must be in [L, cap=%lld], cap <= 2^24",
                (long long)n, (long long)cap);
+  LQ_CHECK_ARG(B * Hkv <= MAX_COUNTERS, "B * Hkv = %lld exceeds %lld", (long long)(B * Hkv),
+               (long long)MAX_COUNTERS);
   LQ_CHECK_ARG(q && kc && ks && kb && vc && vs && vb && out, "null pointer");
   DecodePlan plan;
   QAttnFn fn;
@@ -54,14 +56,18 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  float* part_acc = reinterpret_cast<float*>(workspace);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
+  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
   float2* part_ml = reinterpret_cast<float2*>(part_acc + S * Hq * L * D);
   hipStream_t st = (hipStream_t)stream;
   const float qk = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, q, kc, ks, kb, vc,
-                     vs, vb, (int)Hkv, (int)(Hq / Hkv), (int)L, cap, qk, plan, part_acc, part_ml);
-  LQ_CHECK_LAUNCH("q8_attn_mfma_kernel");
-  launch_merge(part_acc, part_ml, (int)(Hq * L), plan, B, out, st);
-  LQ_CHECK_LAUNCH("decode_merge_kernel");
+                     vs, vb, (int)Hkv, (int)(Hq / Hkv), (int)L, cap, qk, plan, part_acc, part_ml,
+                     counters, out);
+  LQ_CHECK_LAUNCH("q8 attention kernel");
+  if (!attn_merges_itself((Hq / Hkv) * L)) {
+    launch_merge(part_acc, part_ml, (int)(Hq * L), plan, B, out, st);
+    LQ_CHECK_LAUNCH("decode_merge_kernel");
+  }
   return LQ_OK;
 }

@@ -25,12 +25,14 @@ _workspaces: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-(device, stream) scratch buffer, grown on demand. Calls on one stream are ordered,
-    so reuse is safe; different streams get different buffers."""
+    """Per-(device, stream) attention workspace, grown on demand. Calls on one stream are ordered,
+    so reuse is safe; different streams get different buffers. A new buffer starts zeroed: its
+    first LQ_WS_ZERO_BYTES bytes are the kernels' arrival counters, which every call leaves at
+    zero, so only attention calls may use it."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 

@@ -19,11 +19,11 @@ pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-3, 1e-2  # attention tolerance (fp32 accumulate, bf16 output)
 REF_SMALL_N_ATOL = 2e-2  # reference's fused-vs-unfused tolerance (tests/test_q8_attn.py:31)
-NORTH_STAR_MIN_N = 4096
+TIGHT_TOL_MIN_N = 4096
 
 
 def unfused_tol(n):
-    return (ATOL, RTOL) if n >= NORTH_STAR_MIN_N else (REF_SMALL_N_ATOL, 0.0)
+    return (ATOL, RTOL) if n >= TIGHT_TOL_MIN_N else (REF_SMALL_N_ATOL, 0.0)
 
 
 def to_dev_bf16(x, dev):
@@ -210,6 +210,29 @@ def test_ragged_session_lengths_match_single_calls(dev):
         torch.testing.assert_close(got[b:b + 1].float(), one.float(), atol=1e-3, rtol=1e-2)
 
 
+def test_attention_workspace_counters_return_to_zero(dev):
+    """The kernels that merge their own splits count workgroup arrivals in the workspace's leading
+    LQ_WS_ZERO_BYTES bytes; every call must leave them at zero, whatever its shape, so that calls
+    of any shape share one workspace. Repeating a call reproduces it bit for bit."""
+    from lagunalab_amd import _lib
+    from lagunalab_amd import q8_attn as QA
+    rng = np.random.default_rng(21)
+    for B, n, G, Hkv in [(1, 3000, 4, 8), (2, 700, 2, 4), (3, 129, 1, 16), (1, 5000, 4, 8),
+                         (2, 4000, 16, 2)]:
+        cap = (n + 255) // 256 * 256
+        kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+        q = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv * G, 1, 128)), dev)
+        a = QA.decode_attention(q, kq, vq, n=n, scale=0.09)
+        b = QA.decode_attention(q, kq, vq, n=n, scale=0.09)
+        torch.cuda.synchronize()
+        ws = QA._workspaces[(dev, torch.cuda.current_stream(dev).cuda_stream)]
+        assert int(ws[:_lib.LQ_WS_ZERO_BYTES].count_nonzero()) == 0, (B, n, G, Hkv)
+        assert torch.equal(a, b), (B, n, G, Hkv)
+        kn, vn = cache_np(kq), cache_np(vq)
+        qn = q.float().cpu().numpy()
+        assert_attn_close(a, A.fused_attention(qn, kn, vn, n, 0.09), f"B={B} n={n} G={G}")
+
+
 # ---------------------------------------------------------------------------------------------
 # n-gram propose and greedy accept: bit-exact
 # ---------------------------------------------------------------------------------------------
@@ -353,7 +376,8 @@ def test_fused_step_matches_dequantized_path(dev):
 # ---------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,L,G", [(4101, 5, 4), (600, 2, 6), (1000, 8, 2), (300, 16, 4),
-                                   (37, 5, 4), (16, 16, 1), (5000, 3, 8)])
+                                   (37, 5, 4), (16, 16, 1), (5000, 3, 8), (900, 2, 2),
+                                   (1500, 4, 1), (130, 3, 1), (6000, 2, 1)])
 def test_verify_matches_causal_oracle(dev, n, L, G):
     from lagunalab_amd.q8_attn import q8_verify_attention
     rng = np.random.default_rng(n + 7 * L + G)
