@@ -10,8 +10,9 @@ so the 256 MB last-level cache cannot hold the working set. Inputs are synthetic
 HBM before the timed region starts.
 
 Prints one JSON line: value = algorithmic HBM bytes per second over the timed steps (GB/s), the
-roofline of the decode attention kernels (per-call HIP events on the launch stream), and the CPU
-baseline (the oracle's unfused dequantize-to-bf16 + fp32 SDPA path, timed on the host cores).
+roofline of the decode attention kernel (HIP events on the launch stream around groups of
+back-to-back calls after the timed steps), and the CPU baseline (the oracle's unfused
+dequantize-to-bf16 + fp32 SDPA path, timed on the host cores).
 """
 from __future__ import annotations
 
@@ -40,10 +41,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--ctx", type=int, default=82671)
     p.add_argument("--layers", type=int, default=10)
-    p.add_argument("--event-every", type=int, default=8,
-                   help="bracket every K-th timed attention call with events (0: none, and take the "
-                        "roofline from --roofline-calls separate calls after the timed region)")
-    p.add_argument("--roofline-calls", type=int, default=64)
+    p.add_argument("--roofline-calls", type=int, default=128,
+                   help="attention calls timed for the roofline, in groups of 8, after the timed steps")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline sample: calls are repeated until this much time has passed")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -181,16 +180,12 @@ def main():
                                   HQ, HKV, D, cap, n, None, D ** -0.5, out.data_ptr(),
                                   ws.data_ptr(), ws.numel(), sp)
 
-    def step(i, ev=None):
+    def step(i):
         li = i % nl
         off = offsets[li]
         st = append(i, layers[li], off)
         offsets[li] = off + 1
-        if ev is not None:
-            ev[0].record(stream)
         st |= attend(i, layers[li], off + 1)
-        if ev is not None:
-            ev[1].record(stream)
         if st:
             _lib.check(st, "bench step")
         return off + 1
@@ -199,36 +194,35 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # ---- timed region: K steps. Every `event_every`-th step's attention call is bracketed by a
-    # pair of events on the launch stream; the roofline is taken from those calls.
-    every = args.event_every
-    evs = {j: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for j in range(args.steps) if every > 0 and j % every == 0}
+    # ---- timed region: K steps, bracketed by one pair of events on the launch stream
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     ns = []
     torch.cuda.synchronize()
     t_start.record(stream)
     for j in range(args.steps):
-        ns.append(step(args.warmup + j, evs.get(j)))
+        ns.append(step(args.warmup + j))
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    attn_ms = [a.elapsed_time(b) for a, b in evs.values()]
-    attn_n = [ns[j] for j in evs]
-    if not evs:
-        # roofline from a separate pass of event-bracketed attention calls over the same caches
-        pairs = []
-        for j in range(args.roofline_calls):
+
+    # ---- roofline of the attention kernel: groups of 8 back-to-back lq_decode_attn calls (one
+    # kernel launch each) over the rotating caches, one event pair per group on the launch stream.
+    # Per-call time = group time / 8, which includes the short gap between consecutive launches.
+    group = 8
+    pairs, attn_n = [], []
+    for gi in range(max(1, args.roofline_calls // group)):
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record(stream)
+        for k in range(group):
+            j = gi * group + k
             li = j % nl
-            e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            e[0].record(stream)
             _lib.check(attend(j % total_steps, layers[li], offsets[li]), "roofline call")
-            e[1].record(stream)
-            pairs.append(e)
             attn_n.append(offsets[li])
-        torch.cuda.synchronize()
-        attn_ms = [a.elapsed_time(b) for a, b in pairs]
+        e[1].record(stream)
+        pairs.append(e)
+    torch.cuda.synchronize()
+    attn_ms = [a.elapsed_time(b) / group for a, b in pairs]
 
     # per step: K/V codes + scales/biases over n rows, the new bf16 K/V rows read (4096 B), the
     # appended q8 K/V rows written (2176 B), q read and out written (8192 B each)
@@ -264,7 +258,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "lq_decode_attn (q8_attn_packed_kernel, split merge fused)",
-                     "calls_timed": len(attn_ms),
+                     "calls_timed": len(attn_ms) * group,
                      "bytes_per_call": int(sum(attn_bytes) / len(attn_bytes))},
         "vs_baseline_ref": "reference fused q8 kernel on an M4 GPU: 12.24 ms/call = 14.69 GB/s",
     }
