@@ -4,7 +4,8 @@
 
 Workload (one "step" = one decode step of one full-attention layer): quantize-on-append of one new
 bf16 K row and V row (N(0,1), group 64) into the layer's uint8 cache, then fused single-token
-attention of 32 query heads over the 8 KV heads of that layer at n = 82,671 + appended rows.
+attention of 32 query heads over the 8 KV heads of that layer at n = 82,671 + appended rows -- one
+launch of lq_q8_decode_append_attn (the append happens inside the attention kernel).
 Ten distinct layer caches (the real model's 10 full-attention layers, 1.8 GB) rotate step by step
 so the 256 MB last-level cache cannot hold the working set. Inputs are synthetic and resident in
 HBM before the timed region starts.
@@ -46,6 +47,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline sample: calls are repeated until this much time has passed")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--separate-append", action="store_true",
+                   help="append with its own launch (lq_quantize_append_kv) before lq_decode_attn "
+                        "instead of the fused step (lq_q8_decode_append_attn)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
     return p.parse_args()
@@ -167,11 +171,10 @@ def main():
 
     def append(i, lay, off):
         (kc, ks, kb), (vc, vs, vb) = lay
-        st = lib.lq_quantize_append(ks_new[i].data_ptr(), 1, HKV, 1, D, kc.data_ptr(),
-                                    ks.data_ptr(), kb.data_ptr(), cap, off, 8, GS, sp)
-        st |= lib.lq_quantize_append(vs_new[i].data_ptr(), 1, HKV, 1, D, vc.data_ptr(),
-                                     vs.data_ptr(), vb.data_ptr(), cap, off, 8, GS, sp)
-        return st
+        return lib.lq_quantize_append_kv(ks_new[i].data_ptr(), vs_new[i].data_ptr(), 1, HKV, 1, D,
+                                         kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                         vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), cap, off,
+                                         8, GS, sp)
 
     def attend(i, lay, n):
         (kc, ks, kb), (vc, vs, vb) = lay
@@ -180,12 +183,24 @@ def main():
                                   HQ, HKV, D, cap, n, None, D ** -0.5, out.data_ptr(),
                                   ws.data_ptr(), ws.numel(), sp)
 
+    def fused_step(i, lay, off):
+        (kc, ks, kb), (vc, vs, vb) = lay
+        return lib.lq_q8_decode_append_attn(qs[i].data_ptr(), ks_new[i].data_ptr(),
+                                            vs_new[i].data_ptr(), kc.data_ptr(), ks.data_ptr(),
+                                            kb.data_ptr(), vc.data_ptr(), vs.data_ptr(),
+                                            vb.data_ptr(), 1, HQ, HKV, D, cap, off, None,
+                                            D ** -0.5, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                            sp)
+
     def step(i):
         li = i % nl
         off = offsets[li]
-        st = append(i, layers[li], off)
+        if args.separate_append:
+            st = append(i, layers[li], off)
+            st |= attend(i, layers[li], off + 1)
+        else:
+            st = fused_step(i, layers[li], off)
         offsets[li] = off + 1
-        st |= attend(i, layers[li], off + 1)
         if st:
             _lib.check(st, "bench step")
         return off + 1
@@ -247,7 +262,9 @@ def main():
         "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": round(value / REF_M4_GBS, 2), "dtype": "u8",
         "data": "synthetic (N(0,1) bf16 K/V/q, quantized on the GPU)",
-        "config": {"workload": "q8 decode step (append 1 K/V row + fused attention), batch 1, "
+        "config": {"workload": "q8 decode step (append 1 K/V row + fused attention, "
+                               + ("separate append launch" if args.separate_append else "one launch")
+                               + "), batch 1, "
                                f"{HQ}q/{HKV}kv heads, head_dim {D}, group {GS}, context {ctx}, "
                                f"{nl} rotating layer caches",
                    "ctx": ctx, "batch": 1, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,

@@ -59,6 +59,17 @@ int lq_quantize_append(const uint16_t* src, int64_t B, int64_t H, int64_t L, int
                        int64_t offset, int bits, int group_size, void* stream);
 
 /*
+ * Quantize-on-append of the keys and the values of one update in a single launch: the same as
+ * lq_quantize_append on (k_src -> k_*) and on (v_src -> v_*). Replaces the paired mx.quantize of K
+ * and V in QuantizedKVCache.update_and_fetch (laguna_mlx/cache.py:90).
+ */
+int lq_quantize_append_kv(const uint16_t* k_src, const uint16_t* v_src, int64_t B, int64_t H,
+                          int64_t L, int64_t D, uint8_t* k_codes, uint16_t* k_scales,
+                          uint16_t* k_biases, uint8_t* v_codes, uint16_t* v_scales,
+                          uint16_t* v_biases, int64_t cap, int64_t offset, int bits,
+                          int group_size, void* stream);
+
+/*
  * Dequantize rows [0, n) of a cache to bf16 out[B, H, n, D]. Replaces mx.dequantize on the
  * unfused path (laguna_mlx/cache.py:99-100).
  */
@@ -96,6 +107,22 @@ int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const uint16_t* 
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                    const int32_t* lens_host, float scale, uint16_t* out, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/*
+ * One fused single-token decode step on the 8-bit cache: appends the new key and value row of
+ * every sequence (bf16 k_new, v_new [B, Hkv, 1, D], quantized exactly as lq_quantize_append_kv)
+ * at row n (or lens_host[b]) and attends over the n + 1 (lens_host[b] + 1) rows, as
+ * DequantKVCache.update_and_fetch followed by attend on a fused step (laguna_mlx/cache.py:89-92,
+ * 102-106; laguna_mlx/laguna.py:103-105) -- in one kernel launch when Hq / Hkv <= 4. n and
+ * lens_host count the rows BEFORE the append and must leave one free row (< cap). Workspace:
+ * lq_decode_workspace_bytes(LQ_KV_Q8, ...) for the lengths after the append.
+ */
+int lq_q8_decode_append_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                             uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc, uint16_t* vs,
+                             uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                             int64_t cap, int64_t n, const int32_t* lens_host, float scale,
+                             uint16_t* out, void* workspace, int64_t workspace_bytes,
+                             void* stream);
 
 /*
  * Scratch bytes for lq_q8_verify_attn.

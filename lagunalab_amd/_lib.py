@@ -26,10 +26,14 @@ SIGNATURES = {
     "lq_version": (i32, []),
     "lq_last_error": (C.c_char_p, []),
     "lq_quantize_append": (i32, [vp, i64, i64, i64, i64, vp, vp, vp, i64, i64, i32, i32, vp]),
+    "lq_quantize_append_kv": (i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i64, i64,
+                                    i32, i32, vp]),
     "lq_dequantize": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, vp, vp]),
     "lq_decode_workspace_bytes": (i64, [i32, i64, i64, i64, i64, i64, vp]),
     "lq_decode_attn": (i32, [i32, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, vp,
                              f32, vp, vp, i64, vp]),
+    "lq_q8_decode_append_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
+                                       i64, vp, f32, vp, vp, i64, vp]),
     "lq_verify_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64]),
     "lq_q8_verify_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64,
                                 f32, vp, vp, i64, vp]),

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from .quant import dequantize, quantize_into
+from .quant import dequantize, quantize_kv_into
 
 
 def create_attention_mask(N: int, offset: int = 0, return_array: bool = False,
@@ -53,6 +53,18 @@ class QuantizedKVCache:
                 torch.zeros((B, H, rows, D // self.group_size), dtype=torch.bfloat16, device=device))
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        prev = self.reserve(keys, values)
+        quantize_kv_into(keys, values, self.keys, self.values, prev, self.group_size, self.bits)
+        return self.views()
+
+    def views(self):
+        """The first ``offset`` rows of the full-capacity buffers, as returned by update_and_fetch."""
+        return (tuple(t[:, :, :self.offset] for t in self.keys),
+                tuple(t[:, :, :self.offset] for t in self.values))
+
+    def reserve(self, keys: torch.Tensor, values: torch.Tensor) -> int:
+        """Grows the buffers (256-row steps) for ``keys``/``values`` and advances ``offset`` over
+        them without writing them; returns the first row they go to."""
         B, H, L, Dk = keys.shape
         Dv = values.shape[-1]
         prev = self.offset
@@ -70,10 +82,7 @@ class QuantizedKVCache:
                 self.values = tuple(torch.cat([t, z], dim=2) for t, z in
                                     zip(self.values, self._alloc(B, H, new_steps, Dv, values.device)))
         self.offset += L
-        quantize_into(keys, *self.keys, prev, self.group_size, self.bits)
-        quantize_into(values, *self.values, prev, self.group_size, self.bits)
-        return (tuple(t[:, :, :self.offset] for t in self.keys),
-                tuple(t[:, :, :self.offset] for t in self.values))
+        return prev
 
     @property
     def state(self):
@@ -106,10 +115,35 @@ class QuantizedKVCache:
         return sum(t.numel() * t.element_size() for t in (*self.keys, *self.values))
 
 
+class _PendingRows(tuple):
+    """The ``(codes, scales, biases)`` views returned on a fused single-token step. The new row
+    is quantized and written by the following ``attend`` (one fused kernel with the attention);
+    indexing or unpacking this tuple first completes the append, so its contents are always the
+    reference's."""
+
+    def __new__(cls, items, cache):
+        obj = super().__new__(cls, items)
+        obj._cache = cache
+        return obj
+
+    def __getitem__(self, i):
+        self._cache._flush()
+        return super().__getitem__(i)
+
+    def __iter__(self):
+        self._cache._flush()
+        return super().__iter__()
+
+
 class DequantKVCache:
     """Stores K/V quantized and, by default, hands attention dequantized bf16 K/V
     (``laguna_mlx/cache.py:66-144``). No ``bits`` attribute except on single-token
-    ``quantized_decode`` steps."""
+    ``quantized_decode`` steps.
+
+    Fused single-token steps (``fused_decode``): ``update_and_fetch`` reserves the new row and
+    ``attend`` quantizes, stores and attends over it in one kernel launch
+    (``lq_q8_decode_append_attn``). Any other use of the cache before ``attend`` (``state``,
+    ``trim``, the next ``update_and_fetch``, indexing the returned tuples) writes the row first."""
 
     def __init__(self, group_size=64, bits=8, quantized_decode=False, fused_decode=False,
                  fused_verify=None):
@@ -121,12 +155,26 @@ class DequantKVCache:
         self.fused_verify = fused_decode if fused_verify is None else fused_verify
         self._quantized_step = False
         self.fused_step = False
+        self._pending = None  # (keys, values, row) of a fused step until attend() writes it
+
+    def _flush(self):
+        if self._pending is not None:
+            k, v, row = self._pending
+            self._pending = None
+            quantize_kv_into(k, v, self.q.keys, self.q.values, row, self.q.group_size, self.q.bits)
 
     def update_and_fetch(self, keys, values):
-        qk, qv = self.q.update_and_fetch(keys, values)
+        self._flush()
         L = keys.shape[2]
         # Attention checks `fused_step` and then calls attend(); the K/V returned are unused
         self.fused_step = self.fused_decode and (L == 1 or (self.fused_verify and L <= 16))
+        if self.fused_step and L == 1:
+            row = self.q.reserve(keys, values)
+            self._pending = (keys, values, row)
+            self._quantized_step = False
+            qk, qv = self.q.views()
+            return _PendingRows(qk, self), _PendingRows(qv, self)
+        qk, qv = self.q.update_and_fetch(keys, values)
         if self.fused_step:
             self._quantized_step = False
             return qk, qv
@@ -140,10 +188,20 @@ class DequantKVCache:
     def attend(self, queries, scale):
         """Attention straight off the packed cache: the fused decode kernel for one query row,
         the fused causal verify kernel for a block of up to 16 rows."""
-        from .q8_attn import q8_decode_attention, q8_verify_attention
+        from .q8_attn import decode_append_attention, q8_decode_attention, q8_verify_attention
 
         if queries.shape[2] == 1:
+            if self._pending is not None:
+                k, v, row = self._pending
+                B, Hq, L, D = queries.shape
+                if L != 1 or D != 128:
+                    raise AssertionError("decode only, head_dim 128")
+                out = decode_append_attention(queries.to(torch.bfloat16), k, v, self.q.keys,
+                                              self.q.values, n=row, scale=scale)
+                self._pending = None
+                return out.to(queries.dtype)
             return q8_decode_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
+        self._flush()
         return q8_verify_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
 
     @property
@@ -169,12 +227,14 @@ class DequantKVCache:
 
     @property
     def state(self):
+        self._flush()
         return self.q.state
 
     def is_trimmable(self):
         return True
 
     def trim(self, n):
+        self._flush()
         return self.q.trim(n)
 
     def empty(self):

@@ -51,6 +51,19 @@ void clear_error();
 // Compute units of the current device (cached per device id).
 int device_cu_count();
 
+// One tensor to append to a cache: source rows (bf16 [B, H, L, D]) and the cache buffers.
+struct AppendTarget {
+  const uint16_t* src;
+  uint8_t* codes;
+  uint16_t* scales;
+  uint16_t* biases;
+};
+// Quantize-on-append of a (and b when `two`) into rows [offset, offset + L), one launch.
+// Validates its arguments (LQ_EINVAL with the error set).
+int quantize_append(AppendTarget a, AppendTarget b, int two, int64_t B, int64_t H, int64_t L,
+                    int64_t D, int64_t cap, int64_t offset, int bits, int group_size,
+                    hipStream_t st);
+
 // ---------------------------------------------------------------------------------------------
 // device: number formats
 // ---------------------------------------------------------------------------------------------
@@ -63,6 +76,30 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+}
+
+// Affine group quantizer (MLX affine_quantize, restated in oracle/quantize.py): parameters from
+// the group's min and max, then one code per value. IEEE fp32, correctly rounded division, Metal
+// round (halves away from zero). Shared by every kernel that quantizes so that the codes agree
+// bit for bit.
+struct AffineParams {
+  float scale, bias;
+};
+template <int BITS>
+__device__ __forceinline__ AffineParams affine_params(float w_min, float w_max) {
+  constexpr float n_bins = (float)((1 << BITS) - 1);
+  float scale = fmaxf(__fdiv_rn(w_max - w_min, n_bins), 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = roundf(__fdiv_rn(edge, scale));
+  const bool at_zero = q0 == 0.0f;
+  return {at_zero ? scale : __fdiv_rn(edge, q0), at_zero ? 0.0f : edge};
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t affine_code(float x, AffineParams p) {
+  constexpr float n_bins = (float)((1 << BITS) - 1);
+  return (uint32_t)fminf(roundf(__fdiv_rn(x - p.bias, p.scale)), n_bins);
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

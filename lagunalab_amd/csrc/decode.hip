@@ -169,14 +169,16 @@ extern "C" int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, in
   return ws;
 }
 
-extern "C" int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const uint16_t* ks,
-                              const uint16_t* kb, const void* vc, const uint16_t* vs,
-                              const uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                              int64_t cap, int64_t n, const int32_t* lens_host, float scale,
-                              uint16_t* out, void* workspace, int64_t workspace_bytes,
-                              void* stream) {
-  using namespace lq;
-  clear_error();
+namespace lq {
+namespace {
+
+// Decode attention over n (or lens[b]) rows; with k_new/v_new the last row of every sequence is
+// first appended from them (n and lens count the rows after the append).
+int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* kb, void* vc,
+                uint16_t* vs, uint16_t* vb, const uint16_t* k_new, const uint16_t* v_new,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
+                const int32_t* lens, float scale, uint16_t* out, void* workspace,
+                int64_t workspace_bytes, hipStream_t st) {
   LQ_CHECK_ARG(kind == LQ_KV_Q8, "kv kind %d not supported", kind);
   LQ_CHECK_ARG(D == 128, "head_dim must be 128 (got %lld)", (long long)D);
   LQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "Hq=%lld must be a multiple of Hkv=%lld",
@@ -191,25 +193,99 @@ extern "C" int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const
   DecodePlan plan;
   QAttnFn fn;
   int64_t need = 0;
-  const int64_t S = attn_plan(B, Hq, Hkv, 1, n, lens_host, cap, plan, fn, need);
+  const int64_t S = attn_plan(B, Hq, Hkv, 1, n, lens, cap, plan, fn, need);
   LQ_CHECK_ARG(S > 0, "sequence lengths must be in [1, cap=%lld]", (long long)cap);
   if (!workspace || workspace_bytes < need) {
     set_error("workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
-  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
-  float2* part_ml = reinterpret_cast<float2*>(part_acc + S * Hq * D);
-  hipStream_t st = (hipStream_t)stream;
-  const float qk = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, q,
-                     (const uint8_t*)kc, ks, kb, (const uint8_t*)vc, vs, vb, (int)Hkv,
-                     (int)(Hq / Hkv), 1, cap, qk, plan, part_acc, part_ml, counters, out);
+  const bool fused_merge = attn_merges_itself(Hq / Hkv);
+  AttnArgs a{};
+  a.q = q;
+  a.kc = static_cast<uint8_t*>(kc);
+  a.ks = ks;
+  a.kb = kb;
+  a.vc = static_cast<uint8_t*>(vc);
+  a.vs = vs;
+  a.vb = vb;
+  if (k_new) {
+    if (fused_merge) {  // the packed kernel appends the rows itself
+      a.knew = k_new;
+      a.vnew = v_new;
+    } else {  // separate append launch (K and V together), rows len - 1
+      for (int64_t b = 0; b < B; ++b) {
+        const int64_t row = plan.len[b] - 1;
+        const int64_t off = b * Hkv * D;
+        const AppendTarget ta{k_new + off, a.kc + b * Hkv * cap * D, ks + b * Hkv * cap * 2,
+                              kb + b * Hkv * cap * 2};
+        const AppendTarget tb{v_new + off, a.vc + b * Hkv * cap * D, vs + b * Hkv * cap * 2,
+                              vb + b * Hkv * cap * 2};
+        const int rc = quantize_append(ta, tb, 1, 1, Hkv, 1, D, cap, row, 8, 64, st);
+        if (rc != LQ_OK) return rc;
+      }
+    }
+  }
+  a.counters = reinterpret_cast<uint32_t*>(workspace);
+  a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
+  a.part_ml = reinterpret_cast<float2*>(a.part_acc + S * Hq * D);
+  a.out = out;
+  a.cap = cap;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.L = 1;
+  a.qk_scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, a, plan);
   LQ_CHECK_LAUNCH("q8 attention kernel");
-  if (!attn_merges_itself(Hq / Hkv)) {
-    launch_merge(part_acc, part_ml, (int)Hq, plan, B, out, st);
+  if (!fused_merge) {
+    launch_merge(a.part_acc, a.part_ml, (int)Hq, plan, B, out, st);
     LQ_CHECK_LAUNCH("decode_merge_kernel");
   }
   return LQ_OK;
+}
+
+}  // namespace
+}  // namespace lq
+
+extern "C" int lq_decode_attn(int kind, const uint16_t* q, const void* kc, const uint16_t* ks,
+                              const uint16_t* kb, const void* vc, const uint16_t* vs,
+                              const uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                              int64_t cap, int64_t n, const int32_t* lens_host, float scale,
+                              uint16_t* out, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  using namespace lq;
+  clear_error();
+  return decode_attn(kind, q, const_cast<void*>(kc), const_cast<uint16_t*>(ks),
+                     const_cast<uint16_t*>(kb), const_cast<void*>(vc), const_cast<uint16_t*>(vs),
+                     const_cast<uint16_t*>(vb), nullptr, nullptr, B, Hq, Hkv, D, cap, n,
+                     lens_host, scale, out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lq_q8_decode_append_attn(const uint16_t* q, const uint16_t* k_new,
+                                        const uint16_t* v_new, uint8_t* kc, uint16_t* ks,
+                                        uint16_t* kb, uint8_t* vc, uint16_t* vs, uint16_t* vb,
+                                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                        int64_t cap, int64_t n, const int32_t* lens_host,
+                                        float scale, uint16_t* out, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(k_new && v_new, "null pointer");
+  LQ_CHECK_ARG(B >= 1 && B <= LQ_MAX_SEQS, "batch %lld outside [1, %d]", (long long)B, LQ_MAX_SEQS);
+  // lengths after the append: one more row per sequence
+  int32_t after[LQ_MAX_SEQS];
+  if (lens_host) {
+    for (int64_t b = 0; b < B; ++b) {
+      LQ_CHECK_ARG(lens_host[b] >= 0 && lens_host[b] < cap,
+                   "sequence %lld: %d rows leave no room to append in capacity %lld",
+                   (long long)b, lens_host[b], (long long)cap);
+      after[b] = lens_host[b] + 1;
+    }
+  } else {
+    LQ_CHECK_ARG(n >= 0 && n < cap, "n=%lld leaves no room to append in capacity %lld",
+                 (long long)n, (long long)cap);
+  }
+  return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
+                     n + 1, lens_host ? after : nullptr, scale, out, workspace, workspace_bytes,
+                     (hipStream_t)stream);
 }

@@ -25,9 +25,29 @@ __device__ __forceinline__ void find_seq(const DecodePlan& plan, int x, int& b) 
     if (x >= plan.split_begin[i]) b = i;
 }
 
-typedef void (*QAttnFn)(const uint16_t*, const uint8_t*, const uint16_t*, const uint16_t*,
-                        const uint8_t*, const uint16_t*, const uint16_t*, int, int, int, int64_t,
-                        float, DecodePlan, float*, float2*, uint32_t*, uint16_t*);
+// Arguments of the attention kernels (kernel argument block, passed by value).
+struct AttnArgs {
+  const uint16_t* q;  // bf16 [B, Hkv * G, L, D]
+  uint8_t* kc;        // cache buffers of one layer (written only for the fused append)
+  uint16_t* ks;
+  uint16_t* kb;
+  uint8_t* vc;
+  uint16_t* vs;
+  uint16_t* vb;
+  // Fused append (packed kernel only; null otherwise): bf16 rows [B, Hkv, 1, D] that become row
+  // len - 1 of each sequence; the kernel quantizes them, attends over them and stores them.
+  const uint16_t* knew;
+  const uint16_t* vnew;
+  float* part_acc;    // workspace: split partials
+  float2* part_ml;
+  uint32_t* counters; // workspace: arrival counters (zero between calls)
+  uint16_t* out;      // bf16 [B, Hkv * G, L, D]
+  int64_t cap;
+  int Hkv, G, L;
+  float qk_scale_log2;  // softmax scale * log2(e)
+};
+
+typedef void (*QAttnFn)(AttnArgs, DecodePlan);
 
 // Workspace of the attention calls: arrival counters (one per sequence and KV head, zero
 // between calls: each call's last arrival resets its counter) at the start, then the split

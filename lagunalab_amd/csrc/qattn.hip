@@ -134,13 +134,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 template <int NT, bool CAUSAL>
 __global__ __launch_bounds__(NTHR) void q8_attn_mfma_kernel(
-    const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
-    const uint16_t* __restrict__ ks, const uint16_t* __restrict__ kb,
-    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vs,
-    const uint16_t* __restrict__ vb, int Hkv, int G, int L, int64_t cap, float qk_scale_log2,
-    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml,
-    uint32_t* __restrict__ /*counters*/, uint16_t* __restrict__ /*out*/) {
+    AttnArgs args, DecodePlan plan) {
   __shared__ QSmem<NT> sm;
+  const uint16_t* __restrict__ q = args.q;
+  const uint8_t* __restrict__ kc = args.kc;
+  const uint16_t* __restrict__ ks = args.ks;
+  const uint16_t* __restrict__ kb = args.kb;
+  const uint8_t* __restrict__ vc = args.vc;
+  const uint16_t* __restrict__ vs = args.vs;
+  const uint16_t* __restrict__ vb = args.vb;
+  float* __restrict__ part_acc = args.part_acc;
+  float2* __restrict__ part_ml = args.part_ml;
+  const int Hkv = args.Hkv, G = args.G, L = args.L;
+  const int64_t cap = args.cap;
+  const float qk_scale_log2 = args.qk_scale_log2;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -478,6 +485,34 @@ struct PackSmem {
   float st[NWAVE][4][6];
 };
 
+// One 128-element bf16 row quantized to 8 bits in groups of 64 by one wave, lane l holding
+// elements 2l and 2l+1 (group l / 32): the two codes of the lane (low 16 bits) and the bf16 scale
+// and bias of its group. Same arithmetic as quantize_append_kernel (affine_params/affine_code on
+// the group min and max), so the codes agree bit for bit. All 64 lanes must be active.
+struct QPair {
+  uint32_t codes;
+  uint16_t scale, bias;
+};
+__device__ __forceinline__ QPair quantize_pair_q8(uint32_t x2) {
+  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
+  float lo = fminf(x0, x1), hi = fmaxf(x0, x1);
+  lo = fminf(lo, dpp<DPP_QUAD_XOR1>(lo));
+  hi = fmaxf(hi, dpp<DPP_QUAD_XOR1>(hi));
+  lo = fminf(lo, dpp<DPP_QUAD_XOR2>(lo));
+  hi = fmaxf(hi, dpp<DPP_QUAD_XOR2>(hi));
+  lo = fminf(lo, dpp<DPP_ROW_ROR4>(lo));
+  hi = fmaxf(hi, dpp<DPP_ROW_ROR4>(hi));
+  lo = fminf(lo, dpp<DPP_ROW_ROR8>(lo));
+  hi = fmaxf(hi, dpp<DPP_ROW_ROR8>(hi));
+  const auto rl = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(lo), false, false);
+  const auto rh = __builtin_amdgcn_permlane16_swap(__float_as_uint(hi), __float_as_uint(hi), false, false);
+  lo = fminf(__uint_as_float(rl[0]), __uint_as_float(rl[1]));
+  hi = fmaxf(__uint_as_float(rh[0]), __uint_as_float(rh[1]));
+  const AffineParams p = affine_params<8>(lo, hi);
+  return {affine_code<8>(x0, p) | (affine_code<8>(x1, p) << 8), f32_to_bf16(p.scale),
+          f32_to_bf16(p.bias)};
+}
+
 // Agent-scope relaxed atomic accesses: written through to / read from the device-coherent level,
 // so partials published by one workgroup are visible to a workgroup on another XCD without
 // writing back or invalidating a whole L2 (which a fence would do in every workgroup).
@@ -571,14 +606,23 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
-    const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
-    const uint16_t* __restrict__ ks, const uint16_t* __restrict__ kb,
-    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vs,
-    const uint16_t* __restrict__ vb, int Hkv, int G, int L, int64_t cap, float qk_scale_log2,
-    DecodePlan plan, float* __restrict__ part_acc, float2* __restrict__ part_ml,
-    uint32_t* __restrict__ counters, uint16_t* __restrict__ out) {
+    AttnArgs args, DecodePlan plan) {
   __shared__ PackSmem sm;
   __shared__ int sh_last;
+  const uint16_t* __restrict__ q = args.q;
+  const uint8_t* __restrict__ kc = args.kc;
+  const uint16_t* __restrict__ ks = args.ks;
+  const uint16_t* __restrict__ kb = args.kb;
+  const uint8_t* __restrict__ vc = args.vc;
+  const uint16_t* __restrict__ vs = args.vs;
+  const uint16_t* __restrict__ vb = args.vb;
+  float* __restrict__ part_acc = args.part_acc;
+  float2* __restrict__ part_ml = args.part_ml;
+  const int Hkv = args.Hkv, G = args.G, L = args.L;
+  const int64_t cap = args.cap;
+  const float qk_scale_log2 = args.qk_scale_log2;
+  uint32_t* __restrict__ counters = args.counters;
+  uint16_t* __restrict__ out = args.out;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -595,6 +639,13 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const int w_end = min(w_begin + sub, c_end);
   const int nst = (w_end - w_begin + PST - 1) / PST;
   const int R = G * L;  // <= 4
+  // Fused append: the wave whose range holds row n - 1 (the sequence's new last row) quantizes
+  // the new K and V rows itself, patches them into its LDS copy of that super-tile (whatever the
+  // copy read from the cache row is replaced) and stores them to the cache at the end.
+  const int nrow = n - 1;
+  const bool app = args.knew != nullptr && w_begin <= nrow && nrow < w_end;  // wave-uniform
+  const int app_si = app ? (nrow - w_begin) / PST : -1;
+  const int app_r = app ? nrow - (w_begin + app_si * PST) : 0;
   const int Hq = Hkv * G;
   const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
 
@@ -825,6 +876,33 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
     qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
   }
+  QPair app_k = {0u, 0, 0}, app_v = {0u, 0, 0};
+  uint32_t app_w[4] = {0u, 0u, 0u, 0u};  // ks, kb, vs, vb words of the new row (group 0 low)
+  if (app) {
+    const int64_t src = ((int64_t)b * Hkv + hk) * D + 2 * lane;
+    app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(args.knew + src));
+    app_v = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(args.vnew + src));
+    const uint16_t hv[4] = {app_k.scale, app_k.bias, app_v.scale, app_v.bias};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      app_w[j] = (uint32_t)__builtin_amdgcn_readlane((int)hv[j], 0) |
+                 ((uint32_t)__builtin_amdgcn_readlane((int)hv[j], 32) << 16);
+  }
+  // Overwrites row app_r of an LDS super-tile with the new row (same swizzle as the copies:
+  // chunk c of row r at chunk position c ^ (r & 7); lane l holds bytes 2l, 2l+1 = chunk l / 8).
+  auto patch = [&](auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    PackBuf& pb = sm.loop.buf[wv][BUF];
+    const int off = app_r * D + 16 * ((lane >> 3) ^ (app_r & 7)) + 2 * (lane & 7);
+    *reinterpret_cast<uint16_t*>(pb.k + off) = (uint16_t)app_k.codes;
+    *reinterpret_cast<uint16_t*>(pb.v + off) = (uint16_t)app_v.codes;
+    if (lane == 0) {
+      pb.ks[app_r] = app_w[0];
+      pb.kb[app_r] = app_w[1];
+      pb.vs[app_r] = app_w[2];
+      pb.vb[app_r] = app_w[3];
+    }
+  };
 
   // Unrolled by two so that each buffer's LDS offsets are constants. Super-tile si + 1 is always
   // issued before si is processed (past the last super-tile the copies clamp to the wave's last
@@ -833,15 +911,29 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
     issue(si + 1, B1);
     asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile si has landed in LDS
+    if (si == app_si) patch(B0);
     process(si, B0);
     if (si + 1 < nst) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue(si + 2, B0);
       asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+      if (si + 1 == app_si) patch(B1);
       process(si + 1, B1);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (app) {  // the new row goes to the cache (no copy in this kernel reads it back)
+    const int64_t crow = row0 + nrow;
+    *reinterpret_cast<uint16_t*>(args.kc + crow * D + 2 * lane) = (uint16_t)app_k.codes;
+    *reinterpret_cast<uint16_t*>(args.vc + crow * D + 2 * lane) = (uint16_t)app_v.codes;
+    if ((lane & 31) == 0) {
+      const int64_t w = crow * 2 + (lane >> 5);
+      args.ks[w] = app_k.scale;
+      args.kb[w] = app_k.bias;
+      args.vs[w] = app_v.scale;
+      args.vb[w] = app_v.bias;
+    }
+  }
 
   // ---- per-wave totals: sum the 4 key-tile columns of each query row, then the lane groups
 #pragma unroll

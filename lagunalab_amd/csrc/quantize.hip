@@ -17,14 +17,21 @@ namespace {
 constexpr int kWaves = 4;  // waves (groups) per 256-thread block
 
 // EPL: elements per lane (group_size / 64, at least 1). BITS: 4 or 8.
+// Groups [0, ngroups) go to target a, groups [ngroups, 2 ngroups) to target b when `two` (K and
+// V of one update in a single launch).
 template <int EPL, int BITS>
 __global__ __launch_bounds__(256) void quantize_append_kernel(
-    const uint16_t* __restrict__ src, int64_t ngroups, int gs, int groups_per_row, int64_t L,
-    int64_t cap, int64_t offset, uint8_t* __restrict__ codes, uint16_t* __restrict__ scales,
-    uint16_t* __restrict__ biases) {
+    AppendTarget a, AppendTarget b, int two, int64_t ngroups, int gs, int groups_per_row,
+    int64_t L, int64_t cap, int64_t offset) {
   const int lane = threadIdx.x & 63;
-  const int64_t gi = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (gi >= ngroups) return;  // whole wave exits together (gi is wave-uniform)
+  int64_t gi = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (gi >= (two ? 2 * ngroups : ngroups)) return;  // whole wave exits together (wave-uniform)
+  const bool second = gi >= ngroups;
+  if (second) gi -= ngroups;
+  const uint16_t* __restrict__ src = second ? b.src : a.src;
+  uint8_t* __restrict__ codes = second ? b.codes : a.codes;
+  uint16_t* __restrict__ scales = second ? b.scales : a.scales;
+  uint16_t* __restrict__ biases = second ? b.biases : a.biases;
 
   const bool has = lane * EPL < gs;
   float x[EPL];
@@ -41,20 +48,12 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(
   const float w_min = wave_min(lo);
   const float w_max = wave_max(hi);
 
-  constexpr float n_bins = (float)((1 << BITS) - 1);
-  float scale = fmaxf(__fdiv_rn(w_max - w_min, n_bins), 1e-7f);
-  const bool side = fabsf(w_min) > fabsf(w_max);
-  scale = side ? scale : -scale;
-  const float edge = side ? w_min : w_max;
-  const float q0 = roundf(__fdiv_rn(edge, scale));
-  const bool at_zero = q0 == 0.0f;
-  scale = at_zero ? scale : __fdiv_rn(edge, q0);
-  const float bias = at_zero ? 0.0f : edge;
+  const AffineParams p = affine_params<BITS>(w_min, w_max);
+  const float scale = p.scale, bias = p.bias;
 
   uint32_t c[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e)
-    c[e] = (uint32_t)fminf(roundf(__fdiv_rn(x[e] - bias, scale)), n_bins);
+  for (int e = 0; e < EPL; ++e) c[e] = affine_code<BITS>(x[e], p);
 
   // destination row in the cache
   const int64_t row = gi / groups_per_row;
@@ -131,22 +130,18 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
 }
 
 template <int EPL, int BITS>
-void launch_quantize(const uint16_t* src, int64_t ngroups, int gs, int gpr, int64_t L,
-                     int64_t cap, int64_t offset, uint8_t* codes, uint16_t* scales,
-                     uint16_t* biases, hipStream_t st) {
-  const int64_t blocks = (ngroups + kWaves - 1) / kWaves;
+void launch_quantize(AppendTarget a, AppendTarget b, int two, int64_t ngroups, int gs, int gpr,
+                     int64_t L, int64_t cap, int64_t offset, hipStream_t st) {
+  const int64_t blocks = ((two ? 2 : 1) * ngroups + kWaves - 1) / kWaves;
   quantize_append_kernel<EPL, BITS><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-      src, ngroups, gs, gpr, L, cap, offset, codes, scales, biases);
+      a, b, two, ngroups, gs, gpr, L, cap, offset);
 }
 
 }  // namespace
-}  // namespace lq
 
-extern "C" int lq_quantize_append(const uint16_t* src, int64_t B, int64_t H, int64_t L, int64_t D,
-                                  uint8_t* codes, uint16_t* scales, uint16_t* biases, int64_t cap,
-                                  int64_t offset, int bits, int group_size, void* stream) {
-  using namespace lq;
-  clear_error();
+int quantize_append(AppendTarget a, AppendTarget b, int two, int64_t B, int64_t H, int64_t L,
+                    int64_t D, int64_t cap, int64_t offset, int bits, int group_size,
+                    hipStream_t st) {
   LQ_CHECK_ARG(bits == 4 || bits == 8, "bits must be 4 or 8 (got %d)", bits);
   LQ_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
                "group_size must be 32, 64 or 128 (got %d)", group_size);
@@ -156,20 +151,43 @@ extern "C" int lq_quantize_append(const uint16_t* src, int64_t B, int64_t H, int
                (long long)D, group_size);
   LQ_CHECK_ARG(offset >= 0 && offset + L <= cap, "rows [%lld, %lld) exceed capacity %lld",
                (long long)offset, (long long)(offset + L), (long long)cap);
-  LQ_CHECK_ARG(src && codes && scales && biases, "null pointer");
+  LQ_CHECK_ARG(a.src && a.codes && a.scales && a.biases, "null pointer");
+  LQ_CHECK_ARG(!two || (b.src && b.codes && b.scales && b.biases), "null pointer");
   if (L == 0) return LQ_OK;
   const int gpr = (int)(D / group_size);
   const int64_t ngroups = B * H * L * gpr;
-  hipStream_t st = (hipStream_t)stream;
   if (group_size == 128) {
-    if (bits == 8) launch_quantize<2, 8>(src, ngroups, group_size, gpr, L, cap, offset, codes, scales, biases, st);
-    else launch_quantize<2, 4>(src, ngroups, group_size, gpr, L, cap, offset, codes, scales, biases, st);
+    if (bits == 8) launch_quantize<2, 8>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
+    else launch_quantize<2, 4>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
   } else {
-    if (bits == 8) launch_quantize<1, 8>(src, ngroups, group_size, gpr, L, cap, offset, codes, scales, biases, st);
-    else launch_quantize<1, 4>(src, ngroups, group_size, gpr, L, cap, offset, codes, scales, biases, st);
+    if (bits == 8) launch_quantize<1, 8>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
+    else launch_quantize<1, 4>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
   }
   LQ_CHECK_LAUNCH("quantize_append_kernel");
   return LQ_OK;
+}
+
+}  // namespace lq
+
+extern "C" int lq_quantize_append(const uint16_t* src, int64_t B, int64_t H, int64_t L, int64_t D,
+                                  uint8_t* codes, uint16_t* scales, uint16_t* biases, int64_t cap,
+                                  int64_t offset, int bits, int group_size, void* stream) {
+  using namespace lq;
+  clear_error();
+  const AppendTarget a{src, codes, scales, biases};
+  return quantize_append(a, a, 0, B, H, L, D, cap, offset, bits, group_size, (hipStream_t)stream);
+}
+
+extern "C" int lq_quantize_append_kv(const uint16_t* k_src, const uint16_t* v_src, int64_t B,
+                                     int64_t H, int64_t L, int64_t D, uint8_t* k_codes,
+                                     uint16_t* k_scales, uint16_t* k_biases, uint8_t* v_codes,
+                                     uint16_t* v_scales, uint16_t* v_biases, int64_t cap,
+                                     int64_t offset, int bits, int group_size, void* stream) {
+  using namespace lq;
+  clear_error();
+  const AppendTarget a{k_src, k_codes, k_scales, k_biases};
+  const AppendTarget b{v_src, v_codes, v_scales, v_biases};
+  return quantize_append(a, b, 1, B, H, L, D, cap, offset, bits, group_size, (hipStream_t)stream);
 }
 
 extern "C" int lq_dequantize(const uint8_t* codes, const uint16_t* scales, const uint16_t* biases,

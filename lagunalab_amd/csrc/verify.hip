@@ -56,17 +56,28 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
-  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
-  float2* part_ml = reinterpret_cast<float2*>(part_acc + S * Hq * L * D);
+  AttnArgs a{};
+  a.q = q;
+  a.kc = const_cast<uint8_t*>(kc);
+  a.ks = const_cast<uint16_t*>(ks);
+  a.kb = const_cast<uint16_t*>(kb);
+  a.vc = const_cast<uint8_t*>(vc);
+  a.vs = const_cast<uint16_t*>(vs);
+  a.vb = const_cast<uint16_t*>(vb);
+  a.counters = reinterpret_cast<uint32_t*>(workspace);
+  a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
+  a.part_ml = reinterpret_cast<float2*>(a.part_acc + S * Hq * L * D);
+  a.out = out;
+  a.cap = cap;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.L = (int)L;
+  a.qk_scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  const float qk = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, q, kc, ks, kb, vc,
-                     vs, vb, (int)Hkv, (int)(Hq / Hkv), (int)L, cap, qk, plan, part_acc, part_ml,
-                     counters, out);
+  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, a, plan);
   LQ_CHECK_LAUNCH("q8 attention kernel");
   if (!attn_merges_itself((Hq / Hkv) * L)) {
-    launch_merge(part_acc, part_ml, (int)(Hq * L), plan, B, out, st);
+    launch_merge(a.part_acc, a.part_ml, (int)(Hq * L), plan, B, out, st);
     LQ_CHECK_LAUNCH("decode_merge_kernel");
   }
   return LQ_OK;

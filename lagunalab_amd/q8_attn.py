@@ -64,16 +64,8 @@ def _kind_of(keys, D: int) -> int:
     raise ValueError(f"cache rows of {row} bytes do not match head_dim {D} at 8 or 4 bits")
 
 
-def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale: float = None,
-                     lens=None) -> torch.Tensor:
-    """Single-token attention over a quantized (or plain bf16) KV cache.
-
-    q [B, Hq, 1, 128] bf16. ``keys``/``values``: ``(codes, scales, biases)`` of shape
-    ``[B, Hkv, cap, .]`` (8- or 4-bit, group 64), or a plain bf16 tensor ``[B, Hkv, cap, 128]``.
-    Either ``n`` (every sequence has ``n`` valid rows) or ``lens`` (B lengths; ragged batch).
-    Returns ``[B, Hq, 1, 128]`` bf16.
-    """
-    lib = _lib.load()
+def _decode_operands(q, keys, values):
+    """Validated operands of a decode call: (kind, q, (kc, ks, kb), (vc, vs, vb), Hkv, cap)."""
     if not isinstance(keys, (tuple, list)):
         keys, values = (keys, None, None), (values, None, None)
     B, Hq, L, D = q.shape
@@ -82,7 +74,7 @@ def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale:
     kind = _kind_of(keys, D)
     kc, ks, kb = keys
     vc, vs, vb = values
-    dev = _lib.require_device(q, kc, ks, kb, vc, vs, vb)
+    _lib.require_device(q, kc, ks, kb, vc, vs, vb)
     q = _bf16(q, "q")
     if kind == _lib.LQ_KV_BF16:
         kc, vc = _bf16(kc, "keys"), _bf16(vc, "values")
@@ -103,11 +95,32 @@ def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale:
                 raise ValueError(f"scales/biases {tuple(t.shape)} do not match {(B, Hkv, cap, D // 64)}")
     if Hkv < 1 or Hq % Hkv:
         raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} KV heads")
+    return kind, q, (kc, ks, kb), (vc, vs, vb), Hkv, cap
+
+
+def _lens(lens, B):
+    lens_list = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
+    if len(lens_list) != B:
+        raise ValueError(f"lens has {len(lens_list)} entries for a batch of {B}")
+    return lens_list
+
+
+def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale: float = None,
+                     lens=None) -> torch.Tensor:
+    """Single-token attention over a quantized (or plain bf16) KV cache.
+
+    q [B, Hq, 1, 128] bf16. ``keys``/``values``: ``(codes, scales, biases)`` of shape
+    ``[B, Hkv, cap, .]`` (8- or 4-bit, group 64), or a plain bf16 tensor ``[B, Hkv, cap, 128]``.
+    Either ``n`` (every sequence has ``n`` valid rows) or ``lens`` (B lengths; ragged batch).
+    Returns ``[B, Hq, 1, 128]`` bf16.
+    """
+    lib = _lib.load()
+    kind, q, (kc, ks, kb), (vc, vs, vb), Hkv, cap = _decode_operands(q, keys, values)
+    B, Hq, _, D = q.shape
+    dev = q.device
     lens_arr = None
     if lens is not None:
-        lens_list = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
-        if len(lens_list) != B:
-            raise ValueError(f"lens has {len(lens_list)} entries for a batch of {B}")
+        lens_list = _lens(lens, B)
         lens_arr = _lib.C.cast((_lib.C.c_int32 * B)(*lens_list), _lib.C.c_void_p)
         n = 0
     elif n is None:
@@ -124,6 +137,52 @@ def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale:
                             lens_arr, float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
                             _lib.stream_ptr(dev))
     _lib.check(st, "lq_decode_attn")
+    return out
+
+
+def decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, keys,
+                            values, n: int | None = None, scale: float = None,
+                            lens=None) -> torch.Tensor:
+    """One fused decode step on the 8-bit cache: quantize-append the new rows ``k_new``/``v_new``
+    (bf16 ``[B, Hkv, 1, 128]``) at row ``n`` (``lens[b]``) of the full-capacity ``keys``/``values``
+    tuples, then attend over ``n + 1`` (``lens[b] + 1``) rows -- ``update_and_fetch`` followed by
+    ``attend`` (``laguna_mlx/cache.py:89-106``) in one kernel launch when Hq / Hkv <= 4.
+    ``n`` and ``lens`` count the rows before the append. Returns ``[B, Hq, 1, 128]`` bf16."""
+    lib = _lib.load()
+    kind, q, (kc, ks, kb), (vc, vs, vb), Hkv, cap = _decode_operands(q, keys, values)
+    if kind != _lib.LQ_KV_Q8:
+        raise ValueError("the fused decode step runs on the 8-bit cache only")
+    B, Hq, _, D = q.shape
+    dev = q.device
+    _lib.require_device(k_new, v_new)
+    k_new, v_new = _bf16(k_new, "new keys"), _bf16(v_new, "new values")
+    for t in (k_new, v_new):
+        if tuple(t.shape) != (B, Hkv, 1, D):
+            raise ValueError(f"new rows {tuple(t.shape)} do not match {(B, Hkv, 1, D)}")
+    for t in (*keys, *values):
+        if not t.is_contiguous():
+            raise ValueError("the fused decode step writes the cache in place: its buffers must be contiguous")
+    lens_arr = after = None
+    if lens is not None:
+        lens_list = _lens(lens, B)
+        lens_arr = _lib.C.cast((_lib.C.c_int32 * B)(*lens_list), _lib.C.c_void_p)
+        after = _lib.C.cast((_lib.C.c_int32 * B)(*[x + 1 for x in lens_list]), _lib.C.c_void_p)
+        n = 0
+    elif n is None:
+        raise ValueError("give n or lens")
+    if scale is None:
+        scale = D ** -0.5
+    ws_bytes = lib.lq_decode_workspace_bytes(kind, B, Hq, Hkv, D, int(n) + 1, after)
+    if ws_bytes < 0:
+        raise ValueError(lib.lq_last_error().decode())
+    ws = _workspace(dev, ws_bytes)
+    out = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=dev)
+    st = lib.lq_q8_decode_append_attn(q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+                                      kc.data_ptr(), ks.data_ptr(), kb.data_ptr(), vc.data_ptr(),
+                                      vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, D, cap, int(n),
+                                      lens_arr, float(scale), out.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), _lib.stream_ptr(dev))
+    _lib.check(st, "lq_q8_decode_append_attn")
     return out
 
 

@@ -5,7 +5,7 @@ uses them (``laguna_mlx/cache.py:90,100``; ``scripts/micro_kv_decode.py:36``), r
 layout: codes uint8 ``[..., D * bits // 8]`` (8-bit: one byte per element; 4-bit: two per byte,
 even element in the low nibble), bf16 scales and biases ``[..., D // group_size]``.
 ``quantize_into`` is the quantize-on-append primitive: it writes rows ``[offset, offset + L)`` of
-existing full-capacity cache buffers in place.
+existing full-capacity cache buffers in place; ``quantize_kv_into`` does K and V in one launch.
 """
 from __future__ import annotations
 
@@ -21,13 +21,7 @@ def _check_bits(bits, group_size):
         raise ValueError(f"group_size must be 32, 64 or 128, got {group_size}")
 
 
-def quantize_into(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
-                  biases: torch.Tensor, offset: int, group_size: int = 64, bits: int = 8):
-    """Quantize ``x [B, H, L, D]`` (bf16) into rows ``[offset, offset+L)`` of the cache buffers
-    ``codes [B, H, cap, D*bits/8]`` (uint8), ``scales``/``biases [B, H, cap, D/group]`` (bf16)."""
-    lib = _lib.load()
-    _check_bits(bits, group_size)
-    dev = _lib.require_device(x, codes, scales, biases)
+def _check_append(x, codes, scales, biases, group_size, bits):
     if x.dtype != torch.bfloat16:
         raise ValueError(f"K/V rows must be bfloat16, got {x.dtype}")
     if x.dim() != 4:
@@ -43,11 +37,41 @@ def quantize_into(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
     for t in (scales, biases):
         if tuple(t.shape) != want_s or t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError(f"scales/biases must be contiguous bf16 {want_s}")
-    x = x.contiguous()
+    return x.contiguous(), cap
+
+
+def quantize_into(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                  biases: torch.Tensor, offset: int, group_size: int = 64, bits: int = 8):
+    """Quantize ``x [B, H, L, D]`` (bf16) into rows ``[offset, offset+L)`` of the cache buffers
+    ``codes [B, H, cap, D*bits/8]`` (uint8), ``scales``/``biases [B, H, cap, D/group]`` (bf16)."""
+    lib = _lib.load()
+    _check_bits(bits, group_size)
+    dev = _lib.require_device(x, codes, scales, biases)
+    x, cap = _check_append(x, codes, scales, biases, group_size, bits)
+    B, H, L, D = x.shape
     st = lib.lq_quantize_append(x.data_ptr(), B, H, L, D, codes.data_ptr(), scales.data_ptr(),
                                 biases.data_ptr(), cap, int(offset), bits, group_size,
                                 _lib.stream_ptr(dev))
     _lib.check(st, "lq_quantize_append")
+
+
+def quantize_kv_into(k: torch.Tensor, v: torch.Tensor, kbuf, vbuf, offset: int,
+                     group_size: int = 64, bits: int = 8):
+    """:func:`quantize_into` of the keys into ``kbuf`` and of the values into ``vbuf`` (each a
+    ``(codes, scales, biases)`` tuple of one cache) in a single launch."""
+    lib = _lib.load()
+    _check_bits(bits, group_size)
+    dev = _lib.require_device(k, v, *kbuf, *vbuf)
+    k, cap = _check_append(k, *kbuf, group_size, bits)
+    v, cap_v = _check_append(v, *vbuf, group_size, bits)
+    if k.shape != v.shape or cap != cap_v:
+        raise ValueError(f"K {tuple(k.shape)} and V {tuple(v.shape)} rows or capacities differ")
+    B, H, L, D = k.shape
+    st = lib.lq_quantize_append_kv(k.data_ptr(), v.data_ptr(), B, H, L, D, kbuf[0].data_ptr(),
+                                   kbuf[1].data_ptr(), kbuf[2].data_ptr(), vbuf[0].data_ptr(),
+                                   vbuf[1].data_ptr(), vbuf[2].data_ptr(), cap, int(offset), bits,
+                                   group_size, _lib.stream_ptr(dev))
+    _lib.check(st, "lq_quantize_append_kv")
 
 
 def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 8):

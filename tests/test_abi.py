@@ -72,6 +72,23 @@ def test_decode_rejects_bad_arguments(lib):
     assert call(kind=3) == _lib.LQ_EINVAL
 
 
+def test_fused_step_rejects_bad_arguments(lib):
+    from lagunalab_amd import _lib
+    args = dict(q=1, kn=1, vn=1, kc=1, ks=1, kb=1, vc=1, vs=1, vb=1, B=1, Hq=32, Hkv=8, D=128,
+                cap=256, n=10, lens=None, scale=0.1, out=1, ws=1, wsb=1 << 20, st=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.lq_q8_decode_append_attn(*a.values())
+
+    assert call(n=256) == _lib.LQ_EINVAL and b"room" in lib.lq_last_error()  # no free row
+    assert call(kn=None) == _lib.LQ_EINVAL
+    assert call(D=64) == _lib.LQ_EINVAL
+    assert call(B=65) == _lib.LQ_EINVAL
+    st = lib.lq_quantize_append_kv(1, 1, 1, 8, 4, 128, 1, 1, 1, 1, 1, 1, 256, 254, 8, 64, None)
+    assert st == _lib.LQ_EINVAL and b"capacity" in lib.lq_last_error()
+
+
 def test_lookup_ops_reject_bad_arguments(lib):
     from lagunalab_amd import _lib
     assert lib.lq_ngram_propose(1, 100, 0, 4, 1, 1, 64, None) == _lib.LQ_EINVAL

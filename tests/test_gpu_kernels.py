@@ -108,6 +108,29 @@ def test_quantize_append_writes_only_its_rows(dev):
     assert (sc[:, :, :off] == 1.5).all() and (bi[:, :, off + L:] == -2.0).all()
 
 
+@pytest.mark.parametrize("bits,gs", [(8, 64), (4, 64), (8, 128)])
+def test_quantize_kv_one_launch_equals_two(dev, bits, gs):
+    from lagunalab_amd.quant import quantize_into, quantize_kv_into
+    rng = np.random.default_rng(3)
+    B, H, cap, L, off = 2, 4, 96, 7, 33
+    k = to_dev_bf16(Q.randn_bf16(rng, (B, H, L, 128)), dev)
+    v = to_dev_bf16(Q.randn_bf16(rng, (B, H, L, 128)), dev)
+
+    def bufs():
+        return (torch.full((B, H, cap, 128 * bits // 8), 3, dtype=torch.uint8, device=dev),
+                torch.full((B, H, cap, 128 // gs), 0.5, dtype=torch.bfloat16, device=dev),
+                torch.full((B, H, cap, 128 // gs), 0.25, dtype=torch.bfloat16, device=dev))
+    ka, va, kb_, vb_ = bufs(), bufs(), bufs(), bufs()
+    quantize_kv_into(k, v, ka, va, off, gs, bits)
+    quantize_into(k, *kb_, off, gs, bits)
+    quantize_into(v, *vb_, off, gs, bits)
+    for x, y in zip(ka + va, kb_ + vb_):
+        assert torch.equal(x, y)
+    wc, ws, wb = Q.quantize_packed(v.float().cpu().numpy(), gs, bits)
+    np.testing.assert_array_equal(va[0].cpu().numpy()[:, :, off:off + L], wc)
+    np.testing.assert_array_equal(bits16(va[1])[:, :, off:off + L], ws)
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_dequantize_bit_exact(dev, bits):
     from lagunalab_amd.quant import dequantize
@@ -369,6 +392,89 @@ def test_fused_step_matches_dequantized_path(dev):
     qn = q.float().cpu().numpy()
     want = A.sdpa(qn, K.float().cpu().numpy(), V.float().cpu().numpy(), 128 ** -0.5)
     assert_attn_close(got, want.astype(np.float32), "fused vs dequantized", REF_SMALL_N_ATOL, 0.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# fused decode step: quantize-append of the new row inside the attention launch
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,G,B", [(0, 4, 1), (63, 4, 1), (64, 4, 1), (700, 4, 1), (2583, 4, 1),
+                                   (5000, 2, 2), (4095, 1, 1), (1500, 8, 1), (130, 16, 2)])
+def test_fused_decode_step_equals_append_then_attend(dev, n, G, B):
+    """lq_q8_decode_append_attn == lq_quantize_append_kv + lq_decode_attn: the same cache bytes
+    (bit-exact, and equal to the oracle's quantizer) and the same attention output."""
+    from lagunalab_amd.q8_attn import decode_append_attention, decode_attention
+    from lagunalab_amd.quant import quantize_kv_into
+    rng = np.random.default_rng(100 + n + G)
+    Hkv = 8
+    cap = (n + 1 + 255) // 256 * 256
+    kq, vq = make_cache(rng, B, Hkv, max(n, 1), cap, dev)
+    k1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    v1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    q = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv * G, 1, 128)), dev)
+    kf, vf = tuple(t.clone() for t in kq), tuple(t.clone() for t in vq)
+    got = decode_append_attention(q, k1, v1, kf, vf, n=n, scale=0.09)
+    quantize_kv_into(k1, v1, kq, vq, n)
+    want = decode_attention(q, kq, vq, n=n + 1, scale=0.09)
+    for x, y in zip(kf + vf, kq + vq):
+        assert torch.equal(x, y), f"cache differs n={n} G={G}"
+    wc, ws, wb = Q.quantize_packed(k1.float().cpu().numpy(), 64, 8)
+    np.testing.assert_array_equal(kf[0].cpu().numpy()[:, :, n:n + 1], wc)
+    np.testing.assert_array_equal(bits16(kf[2])[:, :, n:n + 1], wb)
+    torch.testing.assert_close(got.float(), want.float(), atol=1e-3, rtol=1e-2)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q.float().cpu().numpy(), kn, vn, n + 1, 0.09),
+                      f"fused step n={n} G={G}")
+
+
+def test_fused_decode_step_ragged(dev):
+    from lagunalab_amd.q8_attn import decode_append_attention, decode_attention
+    from lagunalab_amd.quant import quantize_kv_into
+    rng = np.random.default_rng(41)
+    lens = [61, 0, 2047, 512, 3000]
+    B, Hkv, cap = len(lens), 8, 3072
+    kq, vq = make_cache(rng, B, Hkv, cap, cap, dev)
+    k1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    v1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    q = to_dev_bf16(Q.randn_bf16(rng, (B, 32, 1, 128)), dev)
+    kf, vf = tuple(t.clone() for t in kq), tuple(t.clone() for t in vq)
+    got = decode_append_attention(q, k1, v1, kf, vf, lens=lens, scale=0.09)
+    for b, n in enumerate(lens):
+        quantize_kv_into(k1[b:b + 1], v1[b:b + 1], tuple(t[b:b + 1] for t in kq),
+                         tuple(t[b:b + 1] for t in vq), n)
+    # the slices above are views of contiguous per-sequence blocks: kq now holds every new row
+    want = decode_attention(q, kq, vq, lens=[x + 1 for x in lens], scale=0.09)
+    for x, y in zip(kf + vf, kq + vq):
+        assert torch.equal(x, y)
+    torch.testing.assert_close(got.float(), want.float(), atol=1e-3, rtol=1e-2)
+
+
+def test_fused_step_cache_defers_and_flushes(dev):
+    """DequantKVCache(fused_decode=True): the fused step's cache equals the unfused cache's bytes
+    after attend(); reading the returned tuples before attend() completes the append first."""
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(8)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 8, L, 128)), dev)
+    fused, plain = DequantKVCache(fused_decode=True), DequantKVCache(quantized_decode=True)
+    k0, v0 = kv(255), kv(255)
+    fused.update_and_fetch(k0, v0)
+    plain.update_and_fetch(k0, v0)
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 1, 128)), dev)
+    for step in range(3):  # crosses the 256-row growth step
+        k1, v1 = kv(1), kv(1)
+        fk, fv = fused.update_and_fetch(k1, v1)
+        pk, pv = plain.update_and_fetch(k1, v1)
+        assert fused.fused_step and fused.offset == plain.offset == 256 + step
+        if step == 1:  # touching the returned tuple writes the row now
+            for x, y in zip(fk, pk):
+                assert torch.equal(x, y)
+        a = fused.attend(q, 0.09)
+        from lagunalab_amd.q8_attn import q8_decode_attention
+        b = q8_decode_attention(q, plain.q.keys, plain.q.values, plain.offset, 0.09)
+        torch.testing.assert_close(a.float(), b.float(), atol=1e-3, rtol=1e-2)
+        for x, y in zip(fused.q.keys + fused.q.values, plain.q.keys + plain.q.values):
+            assert torch.equal(x[:, :, :fused.offset], y[:, :, :plain.offset])
+    assert fused.trim(2) == 2 and fused.offset == 256
 
 
 # ---------------------------------------------------------------------------------------------
