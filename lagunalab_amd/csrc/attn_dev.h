@@ -1,0 +1,314 @@
+// Device-side building blocks shared by the attention kernels (qattn.hip, attn_bf16.hip,
+// attn_q4.hip): MFMA operand types and conversions, the global -> LDS copy helpers, agent-scope
+// partial accesses, the row quantizer of the fused append, and the packed kernels' epilogue with
+// the in-kernel split merge.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "qattn.h"
+
+namespace lq {
+namespace attn {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr float RESCALE_LOG2 = 8.0f;  // lazy softmax rescale threshold (log2 units)
+
+// 8 codes (two words) as fp16 subnormals c * 2^-24 for an MFMA operand.
+__device__ __forceinline__ half8_t codes8_sub(uint32_t w0, uint32_t w1) {
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t u = {codes_sub_w(w0, SUB_B01), codes_sub_w(w0, SUB_B23), codes_sub_w(w1, SUB_B01),
+                   codes_sub_w(w1, SUB_B23)};
+  return __builtin_bit_cast(half8_t, u);
+}
+__device__ __forceinline__ half8_t words_as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t u = {a, b, c, d};
+  return __builtin_bit_cast(half8_t, u);
+}
+// Two floats as one dword of fp16 (round to nearest even), x in the low half.
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  const half2_t h = {(_Float16)x, (_Float16)y};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
+
+// Global -> LDS copies (LDS destination = lds_base + size * lane; lds_base wave-uniform). They are
+// issued as inline asm on purpose: the compiler then has no pending LDS write to guard and adds no
+// blanket vmcnt(0) in front of every LDS read, which would wait for the prefetched tile too.
+// Every wait on these copies is explicit (s_waitcnt vmcnt(N) with the count of copies issued
+// after the ones needed).
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ void g2l_b32(const void* g, void* lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(lds_u32(lds_base)) : "memory");
+}
+__device__ __forceinline__ void g2l_b128(const void* g, void* lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(lds_u32(lds_base)) : "memory");
+}
+// Same copies with a wave-uniform global base (SGPR pair) plus a 32-bit per-lane offset, into
+// LDS at lds + LOFF (lds wave-uniform): no 64-bit address arithmetic per lane and no
+// readfirstlane per copy. The instruction's immediate offset stays 0 (it would move the LDS
+// destination too). The asm only moves into M0 (no SCC-writing instruction: the compiler may
+// keep a carry live across the statement).
+template <int LOFF>
+__device__ __forceinline__ void dma_b128(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
+}
+template <int LOFF>
+__device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One 128-element bf16 row quantized to 8 bits in groups of 64 by one wave, lane l holding
+// elements 2l and 2l+1 (group l / 32): the two codes of the lane (low 16 bits) and the bf16 scale
+// and bias of its group. Same arithmetic as quantize_append_kernel (affine_params/affine_code on
+// the group min and max), so the codes agree bit for bit. All 64 lanes must be active.
+struct QPair {
+  uint32_t codes;
+  uint16_t scale, bias;
+};
+__device__ __forceinline__ QPair quantize_pair_q8(uint32_t x2) {
+  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
+  float lo = fminf(x0, x1), hi = fmaxf(x0, x1);
+  lo = fminf(lo, dpp<DPP_QUAD_XOR1>(lo));
+  hi = fmaxf(hi, dpp<DPP_QUAD_XOR1>(hi));
+  lo = fminf(lo, dpp<DPP_QUAD_XOR2>(lo));
+  hi = fmaxf(hi, dpp<DPP_QUAD_XOR2>(hi));
+  lo = fminf(lo, dpp<DPP_ROW_ROR4>(lo));
+  hi = fmaxf(hi, dpp<DPP_ROW_ROR4>(hi));
+  lo = fminf(lo, dpp<DPP_ROW_ROR8>(lo));
+  hi = fmaxf(hi, dpp<DPP_ROW_ROR8>(hi));
+  const auto rl = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(lo), false, false);
+  const auto rh = __builtin_amdgcn_permlane16_swap(__float_as_uint(hi), __float_as_uint(hi), false, false);
+  lo = fminf(__uint_as_float(rl[0]), __uint_as_float(rl[1]));
+  hi = fmaxf(__uint_as_float(rh[0]), __uint_as_float(rh[1]));
+  const AffineParams p = affine_params<8>(lo, hi);
+  return {affine_code<8>(x0, p) | (affine_code<8>(x1, p) << 8), f32_to_bf16(p.scale),
+          f32_to_bf16(p.bias)};
+}
+
+// Agent-scope relaxed atomic accesses: written through to / read from the device-coherent level,
+// so partials published by one workgroup are visible to a workgroup on another XCD without
+// writing back or invalidating a whole L2 (which a fence would do in every workgroup).
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Log-sum-exp merge of the split partials of sequence b, KV head hk (R <= 4 query rows) by one
+// workgroup, into the output rows (b * Hkv + hk) * R + row of out [B, Hq, L, D] (bf16).
+// Partial (m, l, acc) of split s, row r: part_ml / part_acc at (s * Hkv + hk) * R + r.
+// Thread t takes 4 dims (t % 32) of row (t % 128) / 32 over the splits of parity t / 128 (two
+// parities with 4 waves, one with 2): it loads (m, l, acc) of up to MCH splits at once (one
+// memory round trip for up to MCH splits per parity), merges them with its own running max, and
+// the parities meet in LDS. red: LDS scratch of at least 768 floats.
+constexpr int MCH = 16;
+template <int NW>
+__device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& plan,
+                            const float* __restrict__ part_acc,
+                            const float2* __restrict__ part_ml, uint16_t* __restrict__ out,
+                            float* red) {
+  constexpr int NPAR = NW / 2;  // split parities (128 threads each)
+  static_assert(NPAR == 1 || NPAR == 2, "merge_rows4 runs on 2 or 4 waves");
+  const int tid = threadIdx.x;
+  const int s0 = plan.split_begin[b];
+  const int ns = plan.split_begin[b + 1] - s0;
+  const int64_t rs = (int64_t)Hkv * R;
+  const int64_t r0 = (int64_t)hk * R;
+  const float* pml = reinterpret_cast<const float*>(part_ml);
+  const int o = tid & 127;
+  const int row = o >> 5;
+  const int d0 = 4 * (o & 31);
+  const int par = tid >> 7;
+  float M = -INFINITY, den = 0.0f;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if (row < R) {
+    for (int base = par; base < ns; base += NPAR * MCH) {
+      float mv[MCH], lv[MCH], av[MCH][4];
+#pragma unroll
+      for (int k = 0; k < MCH; ++k) {
+        const int sk = min(base + NPAR * k, ns - 1);
+        const int64_t pr = (s0 + sk) * rs + r0 + row;
+        mv[k] = ld_agent(pml + 2 * pr);
+        lv[k] = ld_agent(pml + 2 * pr + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) av[k][j] = ld_agent(part_acc + pr * D + d0 + j);
+      }
+      float cm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < MCH; ++k)
+        if (base + NPAR * k < ns) cm = fmaxf(cm, mv[k]);
+      const float Mn = fmaxf(M, cm);
+      if (Mn != -INFINITY) {
+        const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+        den *= sc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] *= sc;
+#pragma unroll
+        for (int k = 0; k < MCH; ++k) {
+          const float w = (base + NPAR * k < ns && mv[k] != -INFINITY) ? exp2f(mv[k] - Mn) : 0.0f;
+          den += w * lv[k];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[j] += w * av[k][j];
+        }
+        M = Mn;
+      }
+    }
+  }
+  // parity 1 hands (M, den, a) to parity 0 through LDS
+  float M1 = -INFINITY, den1 = 0.0f;
+  float4 a1 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (NPAR == 2) {
+    if (par == 1) {
+      red[o] = M;
+      red[128 + o] = den;
+      *reinterpret_cast<float4*>(red + 256 + 4 * o) = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    __syncthreads();
+    if (par == 0) {
+      M1 = red[o];
+      den1 = red[128 + o];
+      a1 = *reinterpret_cast<const float4*>(red + 256 + 4 * o);
+    }
+  }
+  if (par == 0 && row < R) {
+    const float Mx = fmaxf(M, M1);
+    const float e0 = M == -INFINITY ? 0.0f : exp2f(M - Mx);
+    const float e1 = M1 == -INFINITY ? 0.0f : exp2f(M1 - Mx);
+    const float inv = 1.0f / (e0 * den + e1 * den1);
+    const float r0v = (e0 * a[0] + e1 * a1.x) * inv, r1v = (e0 * a[1] + e1 * a1.y) * inv;
+    const float r2v = (e0 * a[2] + e1 * a1.z) * inv, r3v = (e0 * a[3] + e1 * a1.w) * inv;
+    const uint32_t lo = (uint32_t)f32_to_bf16(r0v) | ((uint32_t)f32_to_bf16(r1v) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(r2v) | ((uint32_t)f32_to_bf16(r3v) << 16);
+    *reinterpret_cast<uint2*>(out + (((int64_t)b * Hkv + hk) * R + row) * D + d0) = make_uint2(lo, hi);
+  }
+}
+
+// Epilogue of the packed kernels. Per wave: the accumulator columns of the 4 key tiles of each
+// query row are summed (lanes 4 and 8 apart in a row), the softmax sum and the two bias sums over
+// all lanes; then the NW waves meet in LDS (acc_lds [NW][4][D], st_lds [NW][4][6]) and their
+// log-sum-exp merge is the workgroup's split partial: acc * out_scale + bias sum of the quant
+// group, written with agent-scope stores. Then the arrival count, and the last workgroup of the
+// (sequence, KV head) merges all splits (merge_rows4). The caller has synchronised the workgroup
+// so that acc_lds/st_lds may overwrite its tile buffers.
+template <int NW>
+__device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bsum0, float bsum1,
+                              float out_scale, float* acc_lds, float* st_lds, int* sh_last,
+                              const AttnArgs& args, const DecodePlan& plan, int x, int b, int hk,
+                              int R) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int lc = lane & 15;
+  const int lq4 = lane >> 4;
+  const int Hkv = args.Hkv;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = oacc[dt][r];
+      v += dpp<DPP_ROW_ROR4>(v);
+      v += dpp<DPP_ROW_ROR8>(v);
+      oacc[dt][r] = v;
+    }
+  float tot[3] = {lsum, bsum0, bsum1};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    float v = tot[k];
+    v += dpp<DPP_ROW_ROR4>(v);
+    v += dpp<DPP_ROW_ROR8>(v);
+    v = sum_xor16(v);
+    v = sum_xor32(v);
+    tot[k] = v;
+  }
+  if (lc < 4) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc_lds[(wv * 4 + lc) * D + 16 * dt + 4 * lq4 + r] = oacc[dt][r];
+    if (lq4 == 0) {
+      float* st = st_lds + (wv * 4 + lc) * 6;
+      st[0] = m_run;
+      st[1] = tot[0];
+      st[2] = tot[1];
+      st[3] = tot[2];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < R * D; o += 64 * NW) {
+    const int col = o / D;
+    const int d = o - col * D;
+    const int g = d >> 6;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, st_lds[(w * 4 + col) * 6]);
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float* st = st_lds + (w * 4 + col) * 6;
+      const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
+      a += e * fmaf(acc_lds[(w * 4 + col) * D + d], out_scale, st[2 + g]);
+    }
+    st_agent(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
+  }
+  if (tid < R) {
+    const int col = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, st_lds[(w * 4 + col) * 6]);
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float* st = st_lds + (w * 4 + col) * 6;
+      l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
+    }
+    float* pml =
+        reinterpret_cast<float*>(args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col);
+    st_agent(pml, M);
+    st_agent(pml + 1, l);
+  }
+
+  // ---- split merge, fused: the last workgroup of (sequence, KV head) to store its partials
+  // merges those of all the sequence's splits and writes the output rows. The partials are
+  // written and read with agent-scope atomics; every thread's stores have completed (vmcnt 0)
+  // before the barrier that precedes the arrival count, and the last workgroup reads only after
+  // its count returned. The last arrival also resets the counter to zero for the next call.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* c = args.counters + b * Hkv + hk;
+    const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
+    const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev + 1 == ns;
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *sh_last = last;
+  }
+  __syncthreads();
+  if (!*sh_last) return;
+  merge_rows4<NW>(b, hk, Hkv, R, plan, args.part_acc, args.part_ml, args.out, acc_lds);
+}
+
+}  // namespace attn
+}  // namespace lq

@@ -106,18 +106,18 @@ int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_
 }
 
 // Resident workgroups per CU for an attention kernel (cached per kernel).
-int attn_occupancy(QAttnFn fn) {
-  static QAttnFn fns[16];
-  static int occ[16];
+int attn_occupancy(QAttnFn fn, int threads) {
+  static QAttnFn fns[32];
+  static int occ[32];
   static int nf = 0;
   for (int i = 0; i < nf; ++i)
     if (fns[i] == fn) return occ[i];
   int k = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, reinterpret_cast<const void*>(fn), 256,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, reinterpret_cast<const void*>(fn), threads,
                                                    0) != hipSuccess ||
       k < 1)
-    k = 2;
-  if (nf < 16) {
+    k = 1;
+  if (nf < 32) {
     fns[nf] = fn;
     occ[nf] = k;
     ++nf;
@@ -135,15 +135,23 @@ void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq
 
 bool attn_merges_itself(int64_t rows_per_kv_head) { return rows_per_kv_head <= 4; }
 
-// Shared by decode (L = 1) and verify (L <= 16): plan + workspace size for the MFMA kernel.
-int64_t attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n, const int32_t* lens,
-                  int64_t cap, DecodePlan& plan, QAttnFn& fn, int64_t& ws_bytes) {
+// Shared by decode (L = 1) and verify (L <= 16): kernel choice, plan and workspace size.
+int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n,
+                  const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
+                  int64_t& ws_bytes) {
   const int64_t R = (Hq / Hkv) * L;
-  const int nt = attn_merges_itself(R) ? 0 : (int)((R + 15) / 16);  // 0: the packed kernel
-  fn = q8_attn_fn(nt, L > 1);
-  if (!fn) return -1;
+  if (kind == LQ_KV_Q8) {
+    const int nt = attn_merges_itself(R) ? 0 : (int)((R + 15) / 16);  // 0: the packed kernel
+    k = {q8_attn_fn(nt, L > 1), 256};
+  } else if (kind == LQ_KV_BF16 && R <= 4) {
+    k = {bf16_attn_fn(L > 1), 128};
+  } else {
+    return -1;
+  }
+  if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
-  const int64_t S = make_plan(B, Hkv, n, lens, cap, attn_occupancy(fn) * device_cu_count(), plan);
+  const int64_t S = make_plan(B, Hkv, n, lens, cap,
+                              attn_occupancy(k.fn, k.threads) * device_cu_count(), plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
   return S;
@@ -155,14 +163,14 @@ extern "C" int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, in
                                              int64_t D, int64_t n, const int32_t* lens_host) {
   using namespace lq;
   clear_error();
-  if (kind != LQ_KV_Q8 || D != 128 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 16) {
+  if (D != 128 || Hkv < 1 || Hq % Hkv || Hq / Hkv > 16) {
     set_error("unsupported decode configuration");
     return -1;
   }
   DecodePlan plan;
-  QAttnFn fn;
+  AttnKernel k;
   int64_t ws = 0;
-  if (attn_plan(B, Hq, Hkv, 1, n, lens_host, 0, plan, fn, ws) < 0) {
+  if (attn_plan(kind, B, Hq, Hkv, 1, n, lens_host, 0, plan, k, ws) < 0) {
     set_error("bad sequence lengths");
     return -1;
   }
@@ -179,7 +187,8 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                 const int32_t* lens, float scale, uint16_t* out, void* workspace,
                 int64_t workspace_bytes, hipStream_t st) {
-  LQ_CHECK_ARG(kind == LQ_KV_Q8, "kv kind %d not supported", kind);
+  LQ_CHECK_ARG(kind == LQ_KV_Q8 || (kind == LQ_KV_BF16 && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
+               "kv kind %d not supported here", kind);
   LQ_CHECK_ARG(D == 128, "head_dim must be 128 (got %lld)", (long long)D);
   LQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "Hq=%lld must be a multiple of Hkv=%lld",
                (long long)Hq, (long long)Hkv);
@@ -189,18 +198,19 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
   LQ_CHECK_ARG(cap >= 1 && cap <= (1 << 24), "capacity %lld outside [1, 2^24]", (long long)cap);
   LQ_CHECK_ARG(B * Hkv <= MAX_COUNTERS, "B * Hkv = %lld exceeds %lld", (long long)(B * Hkv),
                (long long)MAX_COUNTERS);
-  LQ_CHECK_ARG(q && kc && ks && kb && vc && vs && vb && out, "null pointer");
+  LQ_CHECK_ARG(q && kc && vc && out && (kind == LQ_KV_BF16 || (ks && kb && vs && vb)),
+               "null pointer");
   DecodePlan plan;
-  QAttnFn fn;
+  AttnKernel kern;
   int64_t need = 0;
-  const int64_t S = attn_plan(B, Hq, Hkv, 1, n, lens, cap, plan, fn, need);
+  const int64_t S = attn_plan(kind, B, Hq, Hkv, 1, n, lens, cap, plan, kern, need);
   LQ_CHECK_ARG(S > 0, "sequence lengths must be in [1, cap=%lld]", (long long)cap);
   if (!workspace || workspace_bytes < need) {
     set_error("workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  const bool fused_merge = attn_merges_itself(Hq / Hkv);
+  const bool fused_merge = kind == LQ_KV_BF16 || attn_merges_itself(Hq / Hkv);
   AttnArgs a{};
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);
@@ -235,8 +245,9 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
   a.G = (int)(Hq / Hkv);
   a.L = 1;
   a.qk_scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, a, plan);
-  LQ_CHECK_LAUNCH("q8 attention kernel");
+  hipLaunchKernelGGL(kern.fn, dim3((unsigned)S, (unsigned)Hkv), dim3((unsigned)kern.threads), 0,
+                     st, a, plan);
+  LQ_CHECK_LAUNCH("attention kernel");
   if (!fused_merge) {
     launch_merge(a.part_acc, a.part_ml, (int)Hq, plan, B, out, st);
     LQ_CHECK_LAUNCH("decode_merge_kernel");

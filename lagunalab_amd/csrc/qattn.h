@@ -60,10 +60,21 @@ constexpr int64_t MAX_COUNTERS = WS_COUNTER_BYTES / 4;
 // the splits (no decode_merge_kernel launch).
 QAttnFn q8_attn_fn(int nt, bool causal);
 
-// Plan + workspace bytes for an attention call with L query rows per head; returns the number
-// of splits (or -1) and selects the kernel.
-int64_t attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n, const int32_t* lens,
-                  int64_t cap, DecodePlan& plan, QAttnFn& fn, int64_t& ws_bytes);
+// The attention kernel for one call: its function and workgroup size.
+struct AttnKernel {
+  QAttnFn fn;
+  int threads;
+};
+
+// Plain-bf16 cache kernel (attn_bf16.hip), G * L <= 4.
+QAttnFn bf16_attn_fn(bool causal);
+
+// Plan + workspace bytes for an attention call of `kind` (LQ_KV_*) with L query rows per head;
+// returns the number of splits (or -1: bad lengths or an unsupported configuration) and selects
+// the kernel.
+int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n,
+                  const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
+                  int64_t& ws_bytes);
 
 // True when the attention kernel for this many query rows per KV head (G * L) merges the
 // split partials itself (the packed kernel).

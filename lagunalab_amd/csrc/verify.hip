@@ -18,9 +18,9 @@ extern "C" int64_t lq_verify_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv,
     return -1;
   }
   DecodePlan plan;
-  QAttnFn fn;
+  AttnKernel k;
   int64_t ws = 0;
-  if (attn_plan(B, Hq, Hkv, L, n, nullptr, 0, plan, fn, ws) < 0) {
+  if (attn_plan(LQ_KV_Q8, B, Hq, Hkv, L, n, nullptr, 0, plan, k, ws) < 0) {
     set_error("bad sequence length");
     return -1;
   }
@@ -47,9 +47,9 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
                (long long)MAX_COUNTERS);
   LQ_CHECK_ARG(q && kc && ks && kb && vc && vs && vb && out, "null pointer");
   DecodePlan plan;
-  QAttnFn fn;
+  AttnKernel kern;
   int64_t need = 0;
-  const int64_t S = attn_plan(B, Hq, Hkv, L, n, nullptr, cap, plan, fn, need);
+  const int64_t S = attn_plan(LQ_KV_Q8, B, Hq, Hkv, L, n, nullptr, cap, plan, kern, need);
   LQ_CHECK_ARG(S > 0, "bad sequence length");
   if (!workspace || workspace_bytes < need) {
     set_error("workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
@@ -74,7 +74,8 @@ extern "C" int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uin
   a.L = (int)L;
   a.qk_scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(fn, dim3((unsigned)S, (unsigned)Hkv), dim3(256), 0, st, a, plan);
+  hipLaunchKernelGGL(kern.fn, dim3((unsigned)S, (unsigned)Hkv), dim3((unsigned)kern.threads), 0,
+                     st, a, plan);
   LQ_CHECK_LAUNCH("q8 attention kernel");
   if (!attn_merges_itself((Hq / Hkv) * L)) {
     launch_merge(a.part_acc, a.part_ml, (int)(Hq * L), plan, B, out, st);

@@ -395,6 +395,51 @@ def test_fused_step_matches_dequantized_path(dev):
 
 
 # ---------------------------------------------------------------------------------------------
+# plain bf16 cache decode (the bandwidth reference of the quantized paths)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,G,B", [(1, 4, 1), (7, 2, 1), (300, 4, 2), (1000, 1, 1), (4096, 4, 1),
+                                   (5003, 3, 1)])
+def test_bf16_decode_matches_sdpa(dev, n, G, B):
+    from lagunalab_amd.q8_attn import decode_attention
+    rng = np.random.default_rng(200 + n + G)
+    Hkv = 8
+    cap = (n + 255) // 256 * 256
+    k = Q.randn_bf16(rng, (B, Hkv, cap, 128))
+    v = Q.randn_bf16(rng, (B, Hkv, cap, 128))
+    q = Q.randn_bf16(rng, (B, Hkv * G, 1, 128))
+    got = decode_attention(to_dev_bf16(q, dev), to_dev_bf16(k, dev), to_dev_bf16(v, dev), n=n,
+                           scale=128 ** -0.5)
+    assert got.shape == (B, Hkv * G, 1, 128) and got.dtype == torch.bfloat16
+    want = A.sdpa(q, k[:, :, :n], v[:, :, :n], 128 ** -0.5)
+    assert_attn_close(got, want.astype(np.float32), f"bf16 n={n} G={G}")
+
+
+def test_bf16_decode_ragged_and_session_length(dev):
+    from lagunalab_amd.q8_attn import decode_attention
+    g = torch.Generator(device=dev).manual_seed(5)
+    lens = [82671, 42771, 1, 60000]
+    B, cap = len(lens), 82944
+    k = torch.randn(B, 8, cap, 128, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, 8, cap, 128, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
+    got = decode_attention(q, k, v, lens=lens, scale=128 ** -0.5)
+    for b, n in enumerate(lens):
+        qn = q[b:b + 1].float().cpu().numpy()
+        want = A.sdpa(qn, k[b:b + 1, :, :n].float().cpu().numpy(),
+                      v[b:b + 1, :, :n].float().cpu().numpy(), 128 ** -0.5)
+        assert_attn_close(got[b:b + 1], want.astype(np.float32), f"bf16 ragged n={n}")
+
+
+def test_bf16_decode_rejects_large_groups(dev):
+    from lagunalab_amd.q8_attn import decode_attention
+    k = torch.zeros(1, 2, 256, 128, dtype=torch.bfloat16, device=dev)
+    q = torch.zeros(1, 16, 1, 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        decode_attention(q, k, k, n=10)
+
+
+# ---------------------------------------------------------------------------------------------
 # fused decode step: quantize-append of the new row inside the attention launch
 # ---------------------------------------------------------------------------------------------
 
