@@ -213,7 +213,9 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 // group, written with agent-scope stores. Then the arrival count, and the last workgroup of the
 // (sequence, KV head) merges all splits (merge_rows4). The caller has synchronised the workgroup
 // so that acc_lds/st_lds may overwrite its tile buffers.
-template <int NW>
+// EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (row) + p (the 4-bit kernel's P.V
+// operands); otherwise tile j holds dims 16 j + row.
+template <int NW, bool EVEN_ODD = false>
 __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bsum0, float bsum1,
                               float out_scale, float* acc_lds, float* st_lds, int* sh_last,
                               const AttnArgs& args, const DecodePlan& plan, int x, int b, int hk,
@@ -247,7 +249,10 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc_lds[(wv * 4 + lc) * D + 16 * dt + 4 * lq4 + r] = oacc[dt][r];
+      for (int r = 0; r < 4; ++r) {
+        const int dim = EVEN_ODD ? 32 * (dt >> 1) + 2 * (4 * lq4 + r) + (dt & 1) : 16 * dt + 4 * lq4 + r;
+        acc_lds[(wv * 4 + lc) * D + dim] = oacc[dt][r];
+      }
     if (lq4 == 0) {
       float* st = st_lds + (wv * 4 + lc) * 6;
       st[0] = m_run;

@@ -1,0 +1,337 @@
+// Single-token decode attention over the 4-bit cache (group 64, two codes per byte, the even
+// element in the low nibble). The reference refuses a fused 4-bit decode
+// (laguna_mlx/cache.py:81-82) and runs dequantize + SDPA for it (cache.py:99-100,
+// laguna.py:107); this is that computation in one pass over the packed cache.
+//
+// Same plan and structure as the packed 8-bit kernel (qattn.hip), with what 4 bits change:
+//  * A 64-key super-tile is 4 KB of K, 4 KB of V and the four scale/bias word arrays (12 copies);
+//    the whole workgroup needs 80 KB of LDS, so two workgroups share a CU.
+//  * Rows are 64 bytes; chunk c of row r sits at chunk position c ^ ((r >> 2) & 3), which puts
+//    the 16 rows read together in 16 different bank quarters.
+//  * Codes become fp16 subnormals c * 2^-24 after splitting the nibbles (and, shift, and):
+//    one 32-bit word of K (8 dims) is one MFMA step; one ds_read_b64_tr_b8 of V gives every lane
+//    8 keys of two adjacent dims, i.e. two A operands (even and odd dims).
+#include "attn_dev.h"
+
+namespace lq {
+namespace {
+
+using namespace attn;
+
+constexpr int QW = 4;
+constexpr int QTHR = 64 * QW;
+constexpr int QPST = 64;
+constexpr int QROW = D / 2;  // bytes per 4-bit row
+constexpr uint32_t NIB = 0x0f0f0f0fu;
+
+struct Q4Buf {
+  uint8_t k[QPST * QROW];
+  uint8_t v[QPST * QROW];
+  uint32_t ks[QPST];
+  uint32_t kb[QPST];
+  uint32_t vs[QPST];
+  uint32_t vb[QPST];
+};
+
+struct Q4Terms {  // per key of the current super-tile
+  float ks0[QPST], ks1[QPST], ku0[QPST], ku1[QPST];
+  float vs0[QPST], vs1[QPST], vb0[QPST], vb1[QPST];
+};
+
+struct Q4Smem {
+  union {
+    struct {
+      Q4Buf buf[QW][2];
+      Q4Terms terms[QW];
+    } loop;
+    struct {
+      float acc[QW][4][D];
+      float st[QW][4][6];
+      int last;
+    } fin;
+  };
+};
+
+// 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals.
+__device__ __forceinline__ half8_t nib8_sub(uint32_t w) {
+  const uint32_t lo = w & NIB, hi = (w >> 4) & NIB;
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t u = {__builtin_amdgcn_perm(hi, lo, 0x0c040c00u), __builtin_amdgcn_perm(hi, lo, 0x0c050c01u),
+                   __builtin_amdgcn_perm(hi, lo, 0x0c060c02u), __builtin_amdgcn_perm(hi, lo, 0x0c070c03u)};
+  return __builtin_bit_cast(half8_t, u);
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, DecodePlan plan) {
+  __shared__ Q4Smem sm;
+
+  const uint16_t* __restrict__ q = args.q;
+  const uint8_t* __restrict__ kc = args.kc;
+  const uint16_t* __restrict__ ks = args.ks;
+  const uint16_t* __restrict__ kb = args.kb;
+  const uint8_t* __restrict__ vc = args.vc;
+  const uint16_t* __restrict__ vs = args.vs;
+  const uint16_t* __restrict__ vb = args.vb;
+  const int Hkv = args.Hkv, G = args.G, L = args.L;
+  const int64_t cap = args.cap;
+  const float qk_scale_log2 = args.qk_scale_log2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int x = blockIdx.x;
+  const int hk = blockIdx.y;
+  int b;
+  find_seq(plan, x, b);
+  const int n = plan.len[b];
+  const int c_begin = (x - plan.split_begin[b]) * plan.chunk;
+  const int c_end = min(c_begin + plan.chunk, n);
+  const int sub = (c_end - c_begin + QW - 1) / QW;
+  const int w_begin = min(c_begin + wv * sub, c_end);
+  const int w_end = min(w_begin + sub, c_end);
+  const int nst = (w_end - w_begin + QPST - 1) / QPST;
+  const int R = G * L;  // <= 4
+  const int Hq = Hkv * G;
+  const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
+
+  const int lc = lane & 15;
+  const int lq4 = lane >> 4;
+  const int mt = lc >> 2;
+  const int rho = lc & 3;
+  const bool qvalid = rho < R;
+  const int gh = qvalid ? rho / L : 0;
+  const int qi = qvalid ? rho - gh * L : 0;
+  const int causal_bound = n - L + qi;
+
+  half8_t qb[16];
+  float qsum[2];
+  f4_t oacc[8];  // tile 2t + p: dims 32 t + 2 row + p
+  float m_run = -INFINITY, lsum = 0.f, bsum0 = 0.f, bsum1 = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) oacc[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint8_t* kbase = kc + row0 * QROW;
+  const uint8_t* vbase = vc + row0 * QROW;
+  const uint32_t* ksw = reinterpret_cast<const uint32_t*>(ks + row0 * 2);
+  const uint32_t* kbw = reinterpret_cast<const uint32_t*>(kb + row0 * 2);
+  const uint32_t* vsw = reinterpret_cast<const uint32_t*>(vs + row0 * 2);
+  const uint32_t* vbw = reinterpret_cast<const uint32_t*>(vb + row0 * 2);
+  Q4Terms& tm = sm.loop.terms[wv];
+
+  // 12 copies per super-tile: copy u of lane l moves 16 bytes of row 16 u + l / 4, chunk
+  // (l % 4) ^ (l / 16) (= chunk position l % 4 with the row's swizzle), plus the 4 word arrays.
+  const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
+  const uint32_t col_off = (uint32_t)(16 * ((lane & 3) ^ (lane >> 4)));
+  auto issue = [&](int si, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr int OK = offsetof(Q4Buf, k), OV = offsetof(Q4Buf, v);
+    constexpr int OKS = offsetof(Q4Buf, ks), OKB = offsetof(Q4Buf, kb);
+    constexpr int OVS = offsetof(Q4Buf, vs), OVB = offsetof(Q4Buf, vb);
+    const int t0 = w_begin + si * QPST;
+    const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(Q4Buf));
+    const uint8_t* kb0 = kbase;
+    const uint8_t* vb0 = vbase;
+    const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
+    uint32_t ro[4], wo;
+    if (t0 + QPST <= w_end) {
+      kb0 += (int64_t)t0 * QROW;
+      vb0 += (int64_t)t0 * QROW;
+      w0 += t0;
+      w1 += t0;
+      w2 += t0;
+      w3 += t0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ro[u] = (uint32_t)((16 * u + (lane >> 2)) * QROW) + col_off;
+      wo = 4u * (uint32_t)lane;
+    } else {
+      const int last = max(w_end - 1, 0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        ro[u] = (uint32_t)min(t0 + 16 * u + (lane >> 2), last) * QROW + col_off;
+      wo = 4u * (uint32_t)min(t0 + lane, last);
+    }
+    dma_b128<OK + 0>(kb0, ro[0], lb);
+    dma_b128<OV + 0>(vb0, ro[0], lb);
+    dma_b128<OK + 1024>(kb0, ro[1], lb);
+    dma_b128<OV + 1024>(vb0, ro[1], lb);
+    dma_b128<OK + 2048>(kb0, ro[2], lb);
+    dma_b128<OV + 2048>(vb0, ro[2], lb);
+    dma_b128<OK + 3072>(kb0, ro[3], lb);
+    dma_b128<OV + 3072>(vb0, ro[3], lb);
+    dma_b32<OKS>(w0, wo, lb);
+    dma_b32<OKB>(w1, wo, lb);
+    dma_b32<OVS>(w2, wo, lb);
+    dma_b32<OVB>(w3, wo, lb);
+  };
+
+  const uint32_t sel_lo0 = mt == 0 ? ~0u : 0u, sel_hi0 = mt == 1 ? ~0u : 0u;
+  const uint32_t sel_lo1 = mt == 2 ? ~0u : 0u, sel_hi1 = mt == 3 ? ~0u : 0u;
+  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+
+  auto process = [&](int si, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const int t0 = w_begin + si * QPST;
+    const Q4Buf& pb = sm.loop.buf[wv][BUF];
+    {
+      const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
+      tm.ks0[lane] = bf16_lo(a) * kscale;
+      tm.ks1[lane] = bf16_hi(a) * kscale;
+      tm.ku0[lane] = bf16_lo(c);
+      tm.ku1[lane] = bf16_hi(c);
+      tm.vs0[lane] = bf16_lo(e);
+      tm.vs1[lane] = bf16_hi(e);
+      tm.vb0[lane] = bf16_lo(f);
+      tm.vb1[lane] = bf16_hi(f);
+    }
+    // Q.K^T: A = key row lc of tile lq4; chunk c of the row is steps 4c .. 4c + 3 (one word per
+    // 8-dim step); chunks 0-1 are quant group 0, chunks 2-3 group 1 (independent chains).
+    f4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+    {
+      const int r = 16 * lq4 + lc;
+      const int sw = (r >> 2) & 3;
+      const uint8_t* kr = pb.k + r * QROW;
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const uint4 a = *reinterpret_cast<const uint4*>(kr + 16 * (c2 ^ sw));
+        const uint4 g = *reinterpret_cast<const uint4*>(kr + 16 * ((c2 + 2) ^ sw));
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(nib8_sub(aw[j]), qb[4 * c2 + j], c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(nib8_sub(gw[j]), qb[8 + 4 * c2 + j], c1, 0, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int k0 = 16 * mt + 4 * lq4;
+    const float4 ks0 = *reinterpret_cast<const float4*>(tm.ks0 + k0);
+    const float4 ks1 = *reinterpret_cast<const float4*>(tm.ks1 + k0);
+    const float4 ku0 = *reinterpret_cast<const float4*>(tm.ku0 + k0);
+    const float4 ku1 = *reinterpret_cast<const float4*>(tm.ku1 + k0);
+    const float ks0v[4] = {ks0.x, ks0.y, ks0.z, ks0.w}, ks1v[4] = {ks1.x, ks1.y, ks1.z, ks1.w};
+    const float ku0v[4] = {ku0.x, ku0.y, ku0.z, ku0.w}, ku1v[4] = {ku1.x, ku1.y, ku1.z, ku1.w};
+    float sc[4];
+    float tmax = -INFINITY;
+    const bool full = t0 + QPST <= w_end && (!CAUSAL || t0 + QPST - 1 <= n - L);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = fmaf(ks0v[r], c0[r], fmaf(ks1v[r], c1[r], fmaf(ku1v[r], qsum[1], ku0v[r] * qsum[0])));
+      if (!full) {
+        const int t = t0 + k0 + r;
+        bool ok = t < w_end;
+        if (CAUSAL) ok = ok && t <= causal_bound;
+        v = ok ? v : -INFINITY;
+      }
+      sc[r] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
+    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
+    const bool bump = tmax > m_run + RESCALE_LOG2;
+    if (__builtin_amdgcn_ballot_w64(bump)) {
+      const float mn = bump ? tmax : m_run;
+      const float alpha = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
+      m_run = mn;
+      lsum *= alpha;
+      bsum0 *= alpha;
+      bsum1 *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+    }
+    const float mref = m_run == -INFINITY ? 0.0f : m_run;
+    const float4 vs0 = *reinterpret_cast<const float4*>(tm.vs0 + k0);
+    const float4 vs1 = *reinterpret_cast<const float4*>(tm.vs1 + k0);
+    const float4 vb0 = *reinterpret_cast<const float4*>(tm.vb0 + k0);
+    const float4 vb1 = *reinterpret_cast<const float4*>(tm.vb1 + k0);
+    const float vs0v[4] = {vs0.x, vs0.y, vs0.z, vs0.w}, vs1v[4] = {vs1.x, vs1.y, vs1.z, vs1.w};
+    const float vb0v[4] = {vb0.x, vb0.y, vb0.z, vb0.w}, vb1v[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
+      lsum += p[r];
+      bsum0 = fmaf(p[r], vb0v[r], bsum0);
+      bsum1 = fmaf(p[r], vb1v[r], bsum1);
+    }
+    const uint32_t w00 = pack_h2(p[0] * vs0v[0], p[1] * vs0v[1]);
+    const uint32_t w01 = pack_h2(p[2] * vs0v[2], p[3] * vs0v[3]);
+    const uint32_t w10 = pack_h2(p[0] * vs1v[0], p[1] * vs1v[1]);
+    const uint32_t w11 = pack_h2(p[2] * vs1v[2], p[3] * vs1v[3]);
+    // P.V: K-step e covers key tiles 2e (slots 0-3) and 2e+1 (slots 4-7); one transposed read of
+    // 32-dim slab t gives lane lc the bytes of dims 32 t + 2 lc, + 1 for its 8 keys.
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t slo = e == 0 ? sel_lo0 : sel_lo1, shi = e == 0 ? sel_hi0 : sel_hi1;
+      const half8_t b0 = words_as_h8(w00 & slo, w01 & slo, w00 & shi, w01 & shi);
+      const half8_t b1 = words_as_h8(w10 & slo, w11 & slo, w10 & shi, w11 & shi);
+      const int j = lc >> 1;
+      const int key = 16 * (2 * e + (j >> 2)) + 4 * lq4 + (j & 3);
+      const uint8_t* vrow = pb.v + key * QROW + 8 * (lc & 1);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const v2i_t raw =
+            __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (t ^ lq4)));
+        const uint32_t x0 = (uint32_t)raw.x, x1 = (uint32_t)raw.y;
+        const half8_t ae = codes8_sub(x0 & NIB, x1 & NIB);
+        const half8_t ao = codes8_sub((x0 >> 4) & NIB, (x1 >> 4) & NIB);
+        const half8_t& bg = t < 2 ? b0 : b1;
+        oacc[2 * t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, bg, oacc[2 * t], 0, 0, 0);
+        oacc[2 * t + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, bg, oacc[2 * t + 1], 0, 0, 0);
+      }
+    }
+  };
+
+  const std::integral_constant<int, 0> B0;
+  const std::integral_constant<int, 1> B1;
+  issue(0, B0);
+
+  {
+    const bool on = qvalid && mt == lq4;
+    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
+    float sg[2] = {0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * st);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const _Float16 lo = (_Float16)bf16_to_f32((uint16_t)(w[j] & 0xffffu));
+        const _Float16 hi = (_Float16)bf16_to_f32((uint16_t)(w[j] >> 16));
+        qb[st][2 * j] = on ? lo : (_Float16)0.0f;
+        qb[st][2 * j + 1] = on ? hi : (_Float16)0.0f;
+        sg[st >> 3] += (float)lo + (float)hi;
+      }
+    }
+    qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
+    qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
+  }
+
+  for (int si = 0; si < nst; si += 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(si + 1, B1);
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // super-tile si has landed in LDS
+    process(si, B0);
+    if (si + 1 < nst) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(si + 2, B0);
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      process(si + 1, B1);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.fin.acc[0][0][0],
+                          &sm.fin.st[0][0][0], &sm.fin.last, args, plan, x, b, hk, R);
+}
+
+}  // namespace
+
+QAttnFn q4_attn_fn(bool causal) {
+  return causal ? q4_attn_packed_kernel<true> : q4_attn_packed_kernel<false>;
+}
+
+}  // namespace lq

@@ -145,6 +145,8 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
     k = {q8_attn_fn(nt, L > 1), 256};
   } else if (kind == LQ_KV_BF16 && R <= 4) {
     k = {bf16_attn_fn(L > 1), 128};
+  } else if (kind == LQ_KV_Q4 && R <= 4) {
+    k = {q4_attn_fn(L > 1), 256};
   } else {
     return -1;
   }
@@ -187,8 +189,9 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                 const int32_t* lens, float scale, uint16_t* out, void* workspace,
                 int64_t workspace_bytes, hipStream_t st) {
-  LQ_CHECK_ARG(kind == LQ_KV_Q8 || (kind == LQ_KV_BF16 && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
-               "kv kind %d not supported here", kind);
+  LQ_CHECK_ARG(kind == LQ_KV_Q8 ||
+                   ((kind == LQ_KV_BF16 || kind == LQ_KV_Q4) && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
+               "kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
   LQ_CHECK_ARG(D == 128, "head_dim must be 128 (got %lld)", (long long)D);
   LQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "Hq=%lld must be a multiple of Hkv=%lld",
                (long long)Hq, (long long)Hkv);
@@ -210,7 +213,7 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  const bool fused_merge = kind == LQ_KV_BF16 || attn_merges_itself(Hq / Hkv);
+  const bool fused_merge = kind != LQ_KV_Q8 || attn_merges_itself(Hq / Hkv);
   AttnArgs a{};
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);

@@ -68,6 +68,8 @@ struct AttnKernel {
 
 // Plain-bf16 cache kernel (attn_bf16.hip), G * L <= 4.
 QAttnFn bf16_attn_fn(bool causal);
+// 4-bit cache kernel (attn_q4.hip), G * L <= 4.
+QAttnFn q4_attn_fn(bool causal);
 
 // Plan + workspace bytes for an attention call of `kind` (LQ_KV_*) with L query rows per head;
 // returns the number of splits (or -1: bad lengths or an unsupported configuration) and selects

@@ -395,6 +395,51 @@ def test_fused_step_matches_dequantized_path(dev):
 
 
 # ---------------------------------------------------------------------------------------------
+# 4-bit cache decode
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,G,B", [(1, 4, 1), (7, 4, 1), (129, 2, 1), (700, 4, 2), (4096, 4, 1),
+                                   (5003, 1, 1), (9000, 3, 1)])
+def test_q4_decode_matches_oracle(dev, n, G, B):
+    from lagunalab_amd.q8_attn import decode_attention
+    rng = np.random.default_rng(300 + n + G)
+    Hkv = 8
+    cap = (n + 255) // 256 * 256
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev, bits=4)
+    q = Q.randn_bf16(rng, (B, Hkv * G, 1, 128))
+    got = decode_attention(to_dev_bf16(q, dev), kq, vq, n=n, scale=128 ** -0.5)
+    assert got.shape == (B, Hkv * G, 1, 128)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 128 ** -0.5, bits=4),
+                      f"q4 fused n={n} G={G}")
+    at, rt = unfused_tol(n)
+    assert_attn_close(got, A.unfused_attention(q, kn, vn, n, 128 ** -0.5, bits=4),
+                      f"q4 unfused n={n} G={G}", at, rt)
+
+
+def test_q4_decode_ragged_session_lengths(dev):
+    """Ragged 4-bit decode equals one call per sequence at session lengths."""
+    from lagunalab_amd.q8_attn import decode_attention
+    lens = [82671, 42771, 60001]
+    B, cap = len(lens), 82944
+    g = torch.Generator(device=dev).manual_seed(9)
+    mk = lambda: (torch.randint(0, 256, (B, 8, cap, 64), dtype=torch.uint8, device=dev, generator=g),
+                  (torch.rand(B, 8, cap, 2, device=dev, generator=g) * 0.4).to(torch.bfloat16),
+                  (torch.rand(B, 8, cap, 2, device=dev, generator=g) * -3).to(torch.bfloat16))
+    kq, vq = mk(), mk()
+    q = torch.randn(B, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
+    got = decode_attention(q, kq, vq, lens=lens, scale=128 ** -0.5)
+    for b, n in enumerate(lens):
+        one = decode_attention(q[b:b + 1], tuple(t[b:b + 1] for t in kq),
+                               tuple(t[b:b + 1] for t in vq), n=n, scale=128 ** -0.5)
+        torch.testing.assert_close(got[b:b + 1].float(), one.float(), atol=1e-3, rtol=1e-2)
+    kn = tuple(t[2:3].cpu().numpy() if t.dtype == torch.uint8 else bits16(t[2:3]) for t in kq)
+    vn = tuple(t[2:3].cpu().numpy() if t.dtype == torch.uint8 else bits16(t[2:3]) for t in vq)
+    assert_attn_close(got[2:3], A.fused_attention(q[2:3].float().cpu().numpy(), kn, vn, 60001,
+                                                  128 ** -0.5, bits=4), "q4 n=60001")
+
+
+# ---------------------------------------------------------------------------------------------
 # plain bf16 cache decode (the bandwidth reference of the quantized paths)
 # ---------------------------------------------------------------------------------------------
 
