@@ -52,6 +52,13 @@ def parse():
                         "instead of the fused step (lq_q8_decode_append_attn)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
+    p.add_argument("--workload", default="decode",
+                   choices=["decode", "q4", "bf16", "ragged", "verify", "lookup"],
+                   help="decode: the 8-bit decode step (default). q4 / bf16: decode attention over "
+                        "a 4-bit / plain bf16 cache at the same context. ragged: 8 sequences of "
+                        "default_rng(1) lengths in [42771, 82671]. verify: a 5-row causal verify "
+                        "block over 65,536 cached rows plus its append. lookup: n-gram draft search "
+                        "over 82,671 ids and greedy accept of 5 x 131,072 logits")
     return p.parse_args()
 
 
@@ -114,6 +121,341 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n, "copies": 8}), flush=True)
 
 
+# ------------------------------------------------------------------------------------------------
+# the other configurations: same JSON contract, one line each
+# ------------------------------------------------------------------------------------------------
+
+def _cpu_model():
+    try:
+        return [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                if l.startswith("model name")][0]
+    except Exception:
+        return "unknown"
+
+
+def _time_cpu(fn, seconds, min_calls=3):
+    """Median wall time of fn() after one warm-up, repeated for about `seconds`."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_calls or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def _gpu_groups(stream, calls, group, fn):
+    """Per-call ms of `calls` back-to-back fn(j) launches, one event pair per group of `group`."""
+    import torch
+    pairs = []
+    for gi in range(max(1, calls // group)):
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record(stream)
+        for k in range(group):
+            fn(gi * group + k)
+        e[1].record(stream)
+        pairs.append(e)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) / group for a, b in pairs]
+
+
+def _result(metric, value, unit, hib, ms, args, dtype, config, extra):
+    res = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": hib,
+           "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic (N(0,1) bf16 inputs; integer ids uniform)", "config": config}
+    res.update(extra)
+    print(json.dumps(res), flush=True)
+
+
+def run_workload(args):
+    import numpy as np
+    import torch
+
+    from lagunalab_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    g = torch.Generator(device=dev).manual_seed(0)
+    rng = np.random.default_rng(0)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)  # attention workspace, counters at 0
+    scale = D ** -0.5
+    do_cpu = not args.no_cpu_baseline and args.cpu_seconds > 0
+
+    if args.workload in ("q4", "bf16"):
+        # decode attention over 10 rotating layer caches (4-bit: 1152 B/token, bf16: 4096 B/token)
+        n, nl = args.ctx, args.layers
+        cap = (n + 255) // 256 * 256
+        layers = []
+        for _ in range(nl):
+            lay = []
+            for _kv in range(2):
+                x = torch.randn((1, HKV, cap, D), device=dev, generator=g).to(torch.bfloat16)
+                if args.workload == "bf16":
+                    lay.append((x,))
+                    continue
+                codes = torch.empty((1, HKV, cap, D // 2), dtype=torch.uint8, device=dev)
+                sc = torch.empty((1, HKV, cap, 2), dtype=torch.bfloat16, device=dev)
+                bi = torch.empty_like(sc)
+                _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, cap, D, codes.data_ptr(),
+                                                  sc.data_ptr(), bi.data_ptr(), cap, 0, 4, GS, sp),
+                           "prefill quantize")
+                del x
+                lay.append((codes, sc, bi))
+            layers.append(lay)
+        qs = torch.randn((64, 1, HQ, 1, D), device=dev, generator=g).to(torch.bfloat16)
+        out = torch.empty((1, HQ, 1, D), dtype=torch.bfloat16, device=dev)
+        kind = _lib.LQ_KV_BF16 if args.workload == "bf16" else _lib.LQ_KV_Q4
+        per_tok = HKV * (2 * D * 2 if kind == _lib.LQ_KV_BF16 else 2 * (D // 2 + 2 * 2 * (D // GS)))
+        ptr = lambda t, i: t[i].data_ptr() if len(t) > i else None
+
+        def call(j):
+            (k, v) = layers[j % nl]
+            st = lib.lq_decode_attn(kind, qs[j % 64].data_ptr(), k[0].data_ptr(), ptr(k, 1),
+                                    ptr(k, 2), v[0].data_ptr(), ptr(v, 1), ptr(v, 2), 1, HQ, HKV,
+                                    D, cap, n, None, scale, out.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), sp)
+            if st:
+                _lib.check(st, "lq_decode_attn")
+        for j in range(args.warmup):
+            call(j)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for j in range(args.steps):
+            call(j)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        nbytes = per_tok * n + 2 * HQ * D * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        name = "4-bit" if kind == _lib.LQ_KV_Q4 else "plain bf16"
+        extra = {"us_per_call": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                              "kernel": f"lq_decode_attn ({name})", "bytes_per_call": nbytes}}
+        if do_cpu:
+            from oracle import attention as A
+            from oracle import quantize as Q
+            cv = lambda t: (t.cpu().numpy() if t.dtype == torch.uint8
+                            else t.cpu().view(torch.int16).numpy().view(np.uint16))
+            qn = qs[0].float().cpu().numpy()
+            if kind == _lib.LQ_KV_Q4:
+                kh = tuple(cv(t)[:, :, :n] for t in layers[0][0])
+                vh = tuple(cv(t)[:, :, :n] for t in layers[0][1])
+                fn = lambda: A.sdpa(qn, Q.dequantize(*kh, GS, 4), Q.dequantize(*vh, GS, 4), scale,
+                                    dtype=np.float32)
+            else:
+                kf = layers[0][0][0][:, :, :n].float().cpu().numpy()
+                vf = layers[0][1][0][:, :, :n].float().cpu().numpy()
+                fn = lambda: A.sdpa(qn, kf, vf, scale, dtype=np.float32)
+            t, calls = _time_cpu(fn, args.cpu_seconds)
+            extra["cpu_baseline"] = {
+                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "us_per_call": round(t * 1e6, 1),
+                "sample": f"median of {calls} calls of the oracle's {'dequantize + ' if kind == _lib.LQ_KV_Q4 else ''}"
+                          f"fp32 SDPA at n={n}, one layer, one thread; CPU: {_cpu_model()}"}
+        _result(f"{name} decode-attn GB/s at {n}-token ctx", round(gbs, 2), "GB/s", True, ms, args,
+                "u4" if kind == _lib.LQ_KV_Q4 else "bf16",
+                {"workload": f"{name} KV decode attention, batch 1, {HQ}q/{HKV}kv heads, head_dim {D}, "
+                             f"context {n}, {nl} rotating layer caches", "ctx": n, "layers": nl}, extra)
+        return
+
+    if args.workload == "ragged":
+        lens = [int(x) for x in np.random.default_rng(1).integers(42771, 82672, size=8)]
+        B, cap, nl = len(lens), 82944, 3
+        layers = []
+        for _ in range(nl):
+            lay = []
+            for _kv in range(2):
+                codes = torch.randint(0, 256, (B, HKV, cap, D), dtype=torch.uint8, device=dev, generator=g)
+                sc = (torch.rand((B, HKV, cap, 2), device=dev, generator=g) * 0.03).to(torch.bfloat16)
+                bi = (torch.rand((B, HKV, cap, 2), device=dev, generator=g) * -3).to(torch.bfloat16)
+                lay.append((codes, sc, bi))
+            layers.append(lay)
+        q = torch.randn((B, HQ, 1, D), device=dev, generator=g).to(torch.bfloat16)
+        out = torch.empty((B, HQ, 1, D), dtype=torch.bfloat16, device=dev)
+        import ctypes as C
+        lens_arr = C.cast((C.c_int32 * B)(*lens), C.c_void_p)
+
+        def call(j):
+            (kc, ks, kb), (vc, vs, vb) = layers[j % nl]
+            st = lib.lq_decode_attn(8, q.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                    vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, HQ, HKV, D,
+                                    cap, 0, lens_arr, scale, out.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), sp)
+            if st:
+                _lib.check(st, "lq_decode_attn (ragged)")
+        for j in range(args.warmup):
+            call(j)
+        torch.cuda.synchronize()
+        per = _gpu_groups(stream, args.steps, 8, call)
+        ms = sum(per) / len(per)
+        nbytes = Q8_TOKEN * sum(lens) + 2 * B * HQ * D * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        extra = {"us_per_call": round(ms * 1e3, 2), "lens": lens,
+                 "pct_of_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                              "kernel": "lq_decode_attn (8-bit, variable-length splits)",
+                              "bytes_per_call": nbytes}}
+        if do_cpu:  # one sequence, as the reference would run one call per sequence
+            from oracle import attention as A
+            b0 = 4  # the shortest sequence keeps the sample bounded
+            kh = tuple(t[b0:b0 + 1].cpu() for t in layers[0][0])
+            vh = tuple(t[b0:b0 + 1].cpu() for t in layers[0][1])
+            cv = lambda t: t.numpy() if t.dtype == torch.uint8 else t.view(torch.int16).numpy().view(np.uint16)
+            kh, vh = tuple(map(cv, kh)), tuple(map(cv, vh))
+            qn = q[b0:b0 + 1].float().cpu().numpy()
+            fn = lambda: A.unfused_attention(qn, kh, vh, lens[b0], scale)
+            t, calls = _time_cpu(fn, args.cpu_seconds, min_calls=2)
+            extra["cpu_baseline"] = {
+                "value": round(Q8_TOKEN * lens[b0] / t / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port", "us_per_call": round(t * 1e6, 1),
+                "sample": f"median of {calls} oracle calls (dequantize + fp64 SDPA) for one sequence of "
+                          f"{lens[b0]} tokens (the reference runs one call per sequence); CPU: {_cpu_model()}"}
+        _result("q8 ragged decode-attn GB/s, 8 sequences of 42,771-82,671 tokens", round(gbs, 2),
+                "GB/s", True, ms, args, "u8",
+                {"workload": f"ragged 8-bit decode attention, 8 sequences (sum {sum(lens)} tokens), "
+                             f"{HQ}q/{HKV}kv heads, head_dim {D}, {nl} rotating caches",
+                 "batch": B, "layers": nl}, extra)
+        return
+
+    if args.workload == "verify":
+        nc, L, nl = 65536, 5, 10
+        cap = nc + 256
+        layers = []
+        for _ in range(nl):
+            lay = []
+            for _kv in range(2):
+                x = torch.randn((1, HKV, nc, D), device=dev, generator=g).to(torch.bfloat16)
+                codes = torch.zeros((1, HKV, cap, D), dtype=torch.uint8, device=dev)
+                sc = torch.zeros((1, HKV, cap, 2), dtype=torch.bfloat16, device=dev)
+                bi = torch.zeros_like(sc)
+                _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, nc, D, codes.data_ptr(),
+                                                  sc.data_ptr(), bi.data_ptr(), cap, 0, 8, GS, sp),
+                           "prefill quantize")
+                del x
+                lay.append((codes, sc, bi))
+            layers.append(lay)
+        qv = torch.randn((1, HQ, L, D), device=dev, generator=g).to(torch.bfloat16)
+        kn = torch.randn((1, HKV, L, D), device=dev, generator=g).to(torch.bfloat16)
+        vn = torch.randn((1, HKV, L, D), device=dev, generator=g).to(torch.bfloat16)
+        out = torch.empty((1, HQ, L, D), dtype=torch.bfloat16, device=dev)
+
+        def call(j):  # append the 5 block rows at 65,536 (the same rows every call), then verify
+            (kc, ks, kb), (vc, vs, vb) = layers[j % nl]
+            st = lib.lq_quantize_append_kv(kn.data_ptr(), vn.data_ptr(), 1, HKV, L, D, kc.data_ptr(),
+                                           ks.data_ptr(), kb.data_ptr(), vc.data_ptr(), vs.data_ptr(),
+                                           vb.data_ptr(), cap, nc, 8, GS, sp)
+            st |= lib.lq_q8_verify_attn(qv.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                        vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, HQ, HKV, L, D,
+                                        cap, nc + L, scale, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                        sp)
+            if st:
+                _lib.check(st, "verify step")
+        for j in range(args.warmup):
+            call(j)
+        torch.cuda.synchronize()
+        per = _gpu_groups(stream, args.steps, 8, call)
+        ms = sum(per) / len(per)
+        nbytes = Q8_TOKEN * (nc + L) + 2 * HQ * L * D * 2 + 2 * HKV * L * D * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        flops = 4 * (HQ // HKV) * L * D * HKV * (nc + L)
+        extra = {"us_per_call": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
+                 "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                              "kernel": "lq_quantize_append_kv + lq_q8_verify_attn (causal, L=5)",
+                              "bytes_per_call": nbytes}}
+        if do_cpu:
+            from oracle import attention as A
+            cv = lambda t: t.cpu().numpy() if t.dtype == torch.uint8 else t.cpu().view(torch.int16).numpy().view(np.uint16)
+            kh = tuple(cv(t) for t in layers[0][0])
+            vh = tuple(cv(t) for t in layers[0][1])
+            qn = qv.float().cpu().numpy()
+            fn = lambda: A.unfused_attention(qn, kh, vh, nc + L, scale, causal=True)
+            t, calls = _time_cpu(fn, args.cpu_seconds, min_calls=2)
+            extra["cpu_baseline"] = {
+                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "us_per_call": round(t * 1e6, 1),
+                "sample": f"median of {calls} oracle calls (dequantize + causal fp64 SDPA) at "
+                          f"{nc + L} keys, L={L}; CPU: {_cpu_model()}"}
+        _result("q8 verify-attn (q_len 5, causal) GB/s at 65,541 keys", round(gbs, 2), "GB/s",
+                True, ms, args, "u8",
+                {"workload": f"append 5 rows + causal verify attention, {HQ}q/{HKV}kv heads, "
+                             f"head_dim {D}, {nc} cached rows, {nl} rotating caches",
+                 "q_len": L, "ctx": nc + L, "layers": nl}, extra)
+        return
+
+    if args.workload == "lookup":
+        T, gram, nd = 82671, 3, 4
+        h = rng.integers(0, 131072, size=T).astype(np.int32)
+        for s0 in range(0, T - 600, 500):  # a copied 8-gram every ~500 tokens
+            src = int(rng.integers(0, max(1, s0 - 8))) if s0 > 8 else 0
+            h[s0:s0 + 8] = h[src:src + 8]
+        h[-3:] = h[T // 2:T // 2 + 3]
+        hist = torch.from_numpy(h).to(dev)
+        logits = torch.randn((5, 131072), device=dev, generator=g)
+        drafts = logits[:4].argmax(dim=1).to(torch.int32)  # all four drafts accepted
+        nout = torch.empty(2 + nd, dtype=torch.int32, device=dev)
+        aout = torch.empty(2 + 5, dtype=torch.int32, device=dev)
+        nws = torch.empty(max(lib.lq_ngram_workspace_bytes(T), 256), dtype=torch.uint8, device=dev)
+        aws = torch.empty(max(lib.lq_accept_workspace_bytes(5, 131072), 256), dtype=torch.uint8, device=dev)
+
+        def ngram(j):
+            st = lib.lq_ngram_propose(hist.data_ptr(), T, gram, nd, nout.data_ptr(), nws.data_ptr(),
+                                      nws.numel(), sp)
+            if st:
+                _lib.check(st, "lq_ngram_propose")
+
+        def accept(j):
+            st = lib.lq_greedy_accept(logits.data_ptr(), 5, 131072, drafts.data_ptr(), 4,
+                                      aout.data_ptr(), aws.data_ptr(), aws.numel(), sp)
+            if st:
+                _lib.check(st, "lq_greedy_accept")
+        for j in range(args.warmup):
+            ngram(j)
+            accept(j)
+        torch.cuda.synchronize()
+        ng = _gpu_groups(stream, args.steps, 8, ngram)
+        ac = _gpu_groups(stream, args.steps, 8, accept)
+        ng_ms, ac_ms = sum(ng) / len(ng), sum(ac) / len(ac)
+        extra = {"ngram_us_per_call": round(ng_ms * 1e3, 2), "accept_us_per_call": round(ac_ms * 1e3, 2),
+                 "ngram_result": nout.tolist(), "accept_result": aout.tolist()[:2],
+                 "roofline": {"bound": "hbm", "achieved": round((T * 4 + 5 * 131072 * 4) / ((ng_ms + ac_ms) * 1e-3) / 1e9, 1),
+                              "peak": PEAK_GBS, "unit": "GB/s",
+                              "frac": round((T * 4 + 5 * 131072 * 4) / ((ng_ms + ac_ms) * 1e-3) / 1e9 / PEAK_GBS, 5),
+                              "traffic": None, "kernel": "lq_ngram_propose + lq_greedy_accept (latency-bound)",
+                              "bytes_per_call": T * 4 + 5 * 131072 * 4}}
+        if do_cpu:
+            from oracle import lookup as O
+            ids = h.tolist()
+            idx = O.DictIndex(gram)
+            idx.extend(ids)
+            ln = logits.cpu().numpy()
+            dr = drafts.cpu().numpy()
+            t_dict, c1 = _time_cpu(lambda: idx.propose(nd), min(2.0, args.cpu_seconds))
+            t_scan, c2 = _time_cpu(lambda: O.propose_scan(h, T, gram, nd), min(4.0, args.cpu_seconds))
+            t_acc, c3 = _time_cpu(lambda: O.greedy_accept(ln, dr), min(4.0, args.cpu_seconds))
+            extra["cpu_baseline"] = {
+                "value": round((t_scan + t_acc) * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "port",
+                "dict_propose_us": round(t_dict * 1e6, 2), "scan_propose_us": round(t_scan * 1e6, 1),
+                "accept_us": round(t_acc * 1e6, 1),
+                "sample": f"medians of {c1}/{c2}/{c3} calls: the reference's dict NgramIndex.propose "
+                          f"(amortised, index already built), the NumPy backward scan, np.argmax accept; "
+                          f"CPU: {_cpu_model()}"}
+        _result("n-gram draft search (82,671 ids, g=3, n=4) + greedy accept (5 x 131,072) us/call",
+                round((ng_ms + ac_ms) * 1e3, 2), "us", False, ng_ms + ac_ms, args, "int32",
+                {"workload": "prompt-lookup draft search + greedy accept", "history": T, "g": gram,
+                 "n": nd, "vocab": 131072, "rows": 5}, extra)
+        return
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -130,6 +472,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.workload != "decode":
+        run_workload(args)
         return
 
     lib = _lib.load()
