@@ -106,8 +106,8 @@ __device__ __forceinline__ QPair quantize_pair_q8(uint32_t x2) {
 }
 
 // Agent-scope relaxed atomic accesses: written through to / read from the device-coherent level,
-// so partials published by one workgroup are visible to a workgroup on another XCD without
-// writing back or invalidating a whole L2 (which a fence would do in every workgroup).
+// so partials published by one workgroup are visible to a workgroup on another XCD without a
+// release fence (which writes back a whole L2) in every workgroup.
 __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -137,7 +137,6 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
   const int ns = plan.split_begin[b + 1] - s0;
   const int64_t rs = (int64_t)Hkv * R;
   const int64_t r0 = (int64_t)hk * R;
-  const float* pml = reinterpret_cast<const float*>(part_ml);
   const int o = tid & 127;
   const int row = o >> 5;
   const int d0 = 4 * (o & 31);
@@ -151,10 +150,14 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
       for (int k = 0; k < MCH; ++k) {
         const int sk = min(base + NPAR * k, ns - 1);
         const int64_t pr = (s0 + sk) * rs + r0 + row;
-        mv[k] = ld_agent(pml + 2 * pr);
-        lv[k] = ld_agent(pml + 2 * pr + 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) av[k][j] = ld_agent(part_acc + pr * D + d0 + j);
+        const float2 ml = part_ml[pr];
+        const float4 a4 = *reinterpret_cast<const float4*>(part_acc + pr * D + d0);
+        mv[k] = ml.x;
+        lv[k] = ml.y;
+        av[k][0] = a4.x;
+        av[k][1] = a4.y;
+        av[k][2] = a4.z;
+        av[k][3] = a4.w;
       }
       float cm = -INFINITY;
 #pragma unroll
@@ -312,6 +315,9 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
   }
   __syncthreads();
   if (!*sh_last) return;
+  // Acquire: drop this CU's and this XCD's cached lines so that the loads below fetch the
+  // partials the other workgroups wrote through to the device-coherent level.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   merge_rows4<NW>(b, hk, Hkv, R, plan, args.part_acc, args.part_ml, args.out, acc_lds);
 }
 

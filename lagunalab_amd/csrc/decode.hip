@@ -17,6 +17,7 @@ namespace lq {
 namespace {
 
 constexpr int MIN_CHUNK = 128;
+constexpr int64_t MAX_SPLITS = 32;
 
 // ----------------------------------------------------------------------------------------------
 // merge kernel: one workgroup per (sequence, query head), one thread per dim
@@ -93,6 +94,10 @@ int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_
   const int64_t per_head = std::max<int64_t>(1, wgs_target / Hkv);
   int64_t chunk = (total + per_head - 1) / per_head;
   chunk = std::max<int64_t>(chunk, MIN_CHUNK);
+  // at most MAX_SPLITS splits per sequence: the in-kernel merge reads them in one round trip
+  int64_t longest = 0;
+  for (int64_t b = 0; b < B; ++b) longest = std::max<int64_t>(longest, plan.len[b]);
+  chunk = std::max<int64_t>(chunk, (longest + MAX_SPLITS - 1) / MAX_SPLITS);
   chunk = (chunk + 15) / 16 * 16;
   plan.nseq = (int32_t)B;
   plan.chunk = (int32_t)chunk;
