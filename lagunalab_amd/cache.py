@@ -12,7 +12,9 @@ Drop-in for ``laguna_mlx/cache.py``:
   step only; ``fused_decode`` sets ``fused_step`` and ``attend`` runs the fused HIP kernel.
   Extension (``fused_verify``, default: follows ``fused_decode``): multi-token steps of up to 16
   rows -- the speculative verify block -- also take a fused kernel (causal, bottom-right).
-* :func:`make_quantized_cache` -- per-layer factory (``cache.py:147-157``).
+* :func:`make_quantized_cache` -- per-layer factory (``cache.py:147-157``);
+  :func:`make_trimmable_cache` / :class:`TrimmableWindowCache` -- the plain bf16 caches of the
+  speculative loop (``cache.py:7-63``).
 * :class:`RotatingKVCache` -- plain bf16 sliding-window cache for sliding layers (mlx-lm's
   ``RotatingKVCache(max_size=window)``, kept minimal: the last ``max_size`` rows).
 """
@@ -313,7 +315,8 @@ class RotatingKVCache:
         return self.keys, self.values
 
     def make_mask(self, N, return_array=False, window_size=None):
-        stored = 0 if self.keys is None else self.keys.shape[2]
+        # update_and_fetch keeps the last max_size - 1 rows before appending
+        stored = 0 if self.keys is None else min(self.keys.shape[2], self.max_size - 1)
         return create_attention_mask(N, offset=stored, return_array=True,
                                      window_size=window_size or self.max_size)
 
@@ -328,15 +331,80 @@ class RotatingKVCache:
         return 0 if self.keys is None else self.keys.nbytes + self.values.nbytes
 
 
-def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, fused_decode=False):
-    """Quantized KV storage on full-attention layers; sliding layers keep their window."""
+class TrimmableWindowCache:
+    """Sliding-window bf16 cache for speculative decoding (``laguna_mlx/cache.py:7-55``): keeps
+    the last ``window + slack`` rows so that up to ``slack`` rows past the latest update can be
+    trimmed; ``offset`` stays the absolute position."""
+
+    def __init__(self, window, slack=64):
+        self.window, self.slack = window, slack
+        self.keys = self.values = None
+        self.offset = 0
+
+    def _stored(self):
+        return 0 if self.keys is None else min(self.keys.shape[2], self.window + self.slack)
+
+    def update_and_fetch(self, keys, values):
+        if self.keys is None:
+            self.keys, self.values = keys, values
+        else:
+            keep = self.window + self.slack
+            self.keys = torch.cat([self.keys[:, :, -keep:], keys], dim=2)
+            self.values = torch.cat([self.values[:, :, -keep:], values], dim=2)
+        self.offset += keys.shape[2]
+        return self.keys, self.values
+
+    def make_mask(self, N, return_array=False, window_size=None):
+        return create_attention_mask(N, offset=self._stored(), return_array=True,
+                                     window_size=window_size or self.window)
+
+    @property
+    def state(self):
+        return self.keys, self.values
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        n = min(n, 0 if self.keys is None else self.keys.shape[2])
+        if n:
+            self.keys, self.values = self.keys[:, :, :-n], self.values[:, :, :-n]
+            self.offset -= n
+        return n
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def nbytes(self):
+        return 0 if self.keys is None else self.keys.nbytes + self.values.nbytes
+
+
+def make_trimmable_cache(model, slack=64):
+    """Plain bf16 caches that speculative decoding can trim (``laguna_mlx/cache.py:58-63``)."""
+    return [TrimmableWindowCache(model.args.sliding_window, slack)
+            if lt == "sliding_attention" else KVCache()
+            for lt in model.args.layer_types]
+
+
+def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, fused_decode=False,
+                         trim_slack=None):
+    """Quantized KV storage on full-attention layers; sliding layers keep their window
+    (``laguna_mlx/cache.py:147-157``). Extension: with ``trim_slack`` the sliding layers get
+    :class:`TrimmableWindowCache` with that slack, so that every layer can be trimmed and the
+    speculative loop can run over the quantized cache."""
     a = model.args
     if a.head_dim % group_size:
         raise ValueError(f"head_dim {a.head_dim} is not a multiple of group_size {group_size}")
+
+    def window():
+        if trim_slack is None:
+            return RotatingKVCache(max_size=a.sliding_window)
+        return TrimmableWindowCache(a.sliding_window, trim_slack)
+
     return [
-        RotatingKVCache(max_size=a.sliding_window)
-        if lt == "sliding_attention" else DequantKVCache(group_size=group_size, bits=bits,
-                                                         quantized_decode=quantized_decode,
-                                                         fused_decode=fused_decode)
+        window() if lt == "sliding_attention" else DequantKVCache(group_size=group_size, bits=bits,
+                                                                  quantized_decode=quantized_decode,
+                                                                  fused_decode=fused_decode)
         for lt in a.layer_types
     ]

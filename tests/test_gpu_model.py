@@ -1,0 +1,145 @@
+"""Greedy-token identity on a tiny model, through the HIP decode path.
+
+* The fused 8-bit decode cache gives the same logits (within bf16 noise) and argmax as the
+  dequantize-then-SDPA cache (``tests/test_q8_attn.py:35-46`` of the reference).
+* Greedy decoding over the fused cache emits the same tokens as over the dequantizing cache.
+* Prompt-lookup speculative decoding (``generate_lookup``, device ``lq_greedy_accept``) emits
+  exactly ``generate_greedy``'s tokens, both over plain trimmable bf16 caches (the reference's
+  ``tests/test_dflash.py:132-212``) and over the fused quantized cache, whose verify blocks run
+  on the causal verify kernel.
+"""
+import numpy as np
+import pytest
+import torch
+
+from lagunalab_amd import generate as gen
+from lagunalab_amd.cache import make_quantized_cache
+from lagunalab_amd.generate import generate_greedy, generate_lookup
+from tiny_model import TinyLM
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 1024
+PROMPT = [int(t) for t in np.random.default_rng(5).integers(0, VOCAB, size=13)]
+
+
+@pytest.fixture(scope="module")
+def model():
+    # Random models have flat logits (std 40 here, top-2 gaps down to 0.3). With this seed the
+    # fused/unfused deviation of the top-2 difference stays below half the gap at every position
+    # of the greedy runs below, and the echoed prompt yields natural lookup hits.
+    return TinyLM(device="cuda", seed=2)
+
+
+def _quantized(model, fused):
+    # sliding layers trimmable: slack of the largest verify block used here (1 + 15 drafts)
+    return lambda: make_quantized_cache(model, 8, fused_decode=fused, trim_slack=16)
+
+
+def _greedy(model, prompt, n, mk=None, eos=()):
+    return generate_greedy(model, prompt, n, eos=eos, cache=None if mk is None else mk())
+
+
+@torch.no_grad()
+def test_model_decode_matches_dequant_cache(model):
+    ids = torch.tensor([[5, 9, 2, 7, 1, 3, 8, 4] * 40], device="cuda")
+    out = []
+    for fused in (False, True):
+        cache = make_quantized_cache(model, 8, fused_decode=fused)
+        model(ids, cache=cache)
+        tok = torch.tensor([[6]], device="cuda")
+        out.append(torch.cat([model(tok, cache=cache) for _ in range(3)], dim=1))
+    assert (out[0] - out[1]).abs().max().item() < 5e-2 * out[0].abs().max().item()
+    assert torch.equal(out[0].argmax(-1), out[1].argmax(-1))
+
+
+@torch.no_grad()
+def test_fused_greedy_tokens_equal_unfused(model):
+    want = _greedy(model, PROMPT, 40, _quantized(model, False))
+    got = _greedy(model, PROMPT, 40, _quantized(model, True))
+    assert got == want
+
+
+def _echo_prompt(model):
+    # The random model rarely repeats itself; a prompt that echoes its own prefix gives natural
+    # lookup hits at g=2.
+    return PROMPT + generate_greedy(model, PROMPT, 60) + PROMPT
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("fused", [None, True])
+def test_lookup_natural_hits_are_lossless(model, fused):
+    prompt = _echo_prompt(model)
+    mk = None if fused is None else _quantized(model, fused)
+    want = _greedy(model, prompt, 60, mk)
+    got, stats = generate_lookup(model, prompt, 60, g=2, make_cache=mk)
+    assert got == want
+    assert stats["accepted"] > 0 and stats["steps_with_draft"] > 0 and stats["steps"] < 60
+    assert stats["prefill_s"] > 0
+
+
+@torch.no_grad()
+def test_lookup_random_prompt_is_lossless(model):
+    want = generate_greedy(model, PROMPT, 30)
+    got, stats = generate_lookup(model, PROMPT, 30)
+    assert got == want and stats["steps"] > 0
+
+
+@pytest.fixture
+def oracle(monkeypatch):
+    """NgramIndex proposes the true greedy continuation, corrupted from slot ``wrong`` on."""
+
+    def install(truth, wrong=None):
+        def propose(self, n):
+            t = len(self.ids)  # ids = prompt + emitted + pending token
+            out = [int(x) for x in truth[t:t + n]]
+            if wrong is not None:
+                out[wrong:] = [(x + 1) % VOCAB for x in out[wrong:]]
+            return out
+
+        monkeypatch.setattr(gen.NgramIndex, "propose", propose)
+
+    return install
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("fused", [None, True])
+@pytest.mark.parametrize("wrong,expect_accept", [(None, 7), (2, 2)])
+def test_lookup_oracle_accepts_and_stays_lossless(model, oracle, fused, wrong, expect_accept):
+    mk = None if fused is None else _quantized(model, fused)
+    want = _greedy(model, PROMPT, 40, mk)
+    oracle(PROMPT + want, wrong)
+    got, stats = generate_lookup(model, PROMPT, 40, n_draft=7, make_cache=mk)
+    assert got == want
+    assert stats["mean_accepted"] >= expect_accept - 1.5
+
+
+@torch.no_grad()
+def test_lookup_eos_inside_accepted_run(model, oracle):
+    free = generate_greedy(model, PROMPT, 40)
+    eos = (free[17],)
+    want = generate_greedy(model, PROMPT, 40, eos=eos)
+    oracle(PROMPT + free)
+    got, _ = generate_lookup(model, PROMPT, 40, eos=eos)
+    assert got == want and got[-1] == eos[0]
+
+
+@torch.no_grad()
+def test_lookup_max_tokens_mid_block(model, oracle):
+    free = generate_greedy(model, PROMPT, 40)
+    want = generate_greedy(model, PROMPT, 23)
+    oracle(PROMPT + free)
+    got, _ = generate_lookup(model, PROMPT, 23)
+    assert got == want
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("wrong", [None, 1])
+def test_lookup_adaptive_is_lossless(model, oracle, wrong):
+    mk = _quantized(model, True)
+    want = _greedy(model, PROMPT, 40, mk)
+    oracle(PROMPT + want, wrong)
+    got, stats = generate_lookup(model, PROMPT, 40, n_draft=15, adaptive=True, make_cache=mk)
+    assert got == want
+    if wrong == 1:  # the cap is 1 + previous accepted = 2 after the first step
+        assert stats["drafted"] <= 15 + 2 * (stats["steps"] - 1)
