@@ -93,7 +93,8 @@ int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, 
  * Fused single-token decode attention. Replaces q8_decode_attention(q, keys, values, n, scale)
  * (laguna_mlx/q8_attn.py:102-130: the Metal kernel N1 at :17-99 and the block merge at
  * :126-130) and generalises it to 4-bit and plain-bf16 caches and to ragged batches.
- *   q    bf16 [B, Hq, 1, D] contiguous, D == 128, Hq % Hkv == 0, Hq / Hkv <= 16
+ *   q    bf16 [B, Hq, 1, D] contiguous, D == 128, Hq % Hkv == 0, Hq / Hkv <= 16 (<= 4 for
+ *        LQ_KV_Q4 and LQ_KV_BF16)
  *   kc..vb the cache buffers of one layer (layout above; for LQ_KV_BF16, kc and vc are bf16
  *          [B, Hkv, cap, D])
  *   n    valid rows when lens_host == NULL; otherwise lens_host[b] (host array, B <= 64,

@@ -174,6 +174,10 @@ extern "C" int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, in
     set_error("unsupported decode configuration");
     return -1;
   }
+  if (kind != LQ_KV_Q8 && !((kind == LQ_KV_BF16 || kind == LQ_KV_Q4) && Hq / Hkv <= 4)) {
+    set_error("kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
+    return -1;
+  }
   DecodePlan plan;
   AttnKernel k;
   int64_t ws = 0;
