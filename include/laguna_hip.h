@@ -36,11 +36,12 @@ extern "C" {
 
 /*
  * Attention workspaces (lq_decode_attn, lq_q8_verify_attn) start with LQ_WS_ZERO_BYTES bytes of
- * arrival counters that must be zero before the first call that uses the workspace (clear them
- * once after allocating it); every call leaves them zero again. Calls that share a workspace
- * must be ordered (one stream). At most LQ_WS_ZERO_BYTES / 4 (sequence, KV head) pairs per call.
+ * counters (per sequence and KV head: an arrival count and a work-distribution count) that must
+ * be zero before the first call that uses the workspace (clear them once after allocating it);
+ * every call leaves them zero again. Calls that share a workspace must be ordered (one stream).
+ * At most 2048 (sequence, KV head) pairs per call.
  */
-#define LQ_WS_ZERO_BYTES 16384
+#define LQ_WS_ZERO_BYTES 139264
 
 /* Library version (major*10000 + minor*100 + patch). */
 int lq_version(void);

@@ -300,9 +300,10 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
 
   // ---- split merge, fused: the last workgroup of (sequence, KV head) to store its partials
   // merges those of all the sequence's splits and writes the output rows. The partials are
-  // written and read with agent-scope atomics; every thread's stores have completed (vmcnt 0)
-  // before the barrier that precedes the arrival count, and the last workgroup reads only after
-  // its count returned. The last arrival also resets the counter to zero for the next call.
+  // written with agent-scope stores; every thread's stores (and its wave's last tile-counter
+  // grab) have completed (vmcnt 0) before the barrier that precedes the arrival count, and the
+  // last workgroup reads only after its count returned. The last arrival also resets the
+  // arrival and tile counters to zero for the next call.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
@@ -310,7 +311,12 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
     const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev + 1 == ns;
-    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) {  // every workgroup of (b, hk) is past its loop: reset both counters
+      uint32_t* tc = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(args.counters) +
+                                                 TILE_CTR_BYTES + TILE_CTR_STRIDE * (b * Hkv + hk));
+      __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(tc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     *sh_last = last;
   }
   __syncthreads();

@@ -40,7 +40,7 @@ struct AttnArgs {
   const uint16_t* vnew;
   float* part_acc;    // workspace: split partials
   float2* part_ml;
-  uint32_t* counters; // workspace: arrival counters (zero between calls)
+  uint32_t* counters; // workspace: arrival and tile counters (zero between calls)
   uint16_t* out;      // bf16 [B, Hkv * G, L, D]
   int64_t cap;
   int Hkv, G, L;
@@ -49,11 +49,17 @@ struct AttnArgs {
 
 typedef void (*QAttnFn)(AttnArgs, DecodePlan);
 
-// Workspace of the attention calls: arrival counters (one per sequence and KV head, zero
-// between calls: each call's last arrival resets its counter) at the start, then the split
-// partials. The counter area has a fixed size so that calls of any shape can share a workspace.
+// Workspace of the attention calls: per sequence and KV head i an arrival counter (uint32 at
+// 4 i) and a tile counter of the packed kernels (uint32 at TILE_CTR_BYTES + TILE_CTR_STRIDE i,
+// one per 64-byte line: atomics on one line serialize), both zero between calls (each call's
+// last arrival resets them), then the split partials. The counter area has a fixed size so that
+// calls of any shape can share a workspace.
 constexpr int64_t WS_COUNTER_BYTES = LQ_WS_ZERO_BYTES;
-constexpr int64_t MAX_COUNTERS = WS_COUNTER_BYTES / 4;
+constexpr int64_t MAX_COUNTERS = 2048;
+constexpr int TILE_CTR_BYTES = 4 * MAX_COUNTERS;
+constexpr int TILE_CTR_STRIDE = 64;
+static_assert(TILE_CTR_BYTES + TILE_CTR_STRIDE * MAX_COUNTERS <= WS_COUNTER_BYTES,
+              "counter area too small");
 
 // MFMA attention kernel for `nt` 16-column tiles of query rows (G * L <= 16 * nt), causal for
 // multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4, which also merges

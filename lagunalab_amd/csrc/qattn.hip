@@ -446,20 +446,24 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   int b;
   find_seq(plan, x, b);
   const int n = plan.len[b];
-  const int c_begin = (x - plan.split_begin[b]) * plan.chunk;
-  const int c_end = min(c_begin + plan.chunk, n);
-  const int sub = (c_end - c_begin + NWAVE - 1) / NWAVE;
-  const int w_begin = min(c_begin + wv * sub, c_end);
-  const int w_end = min(w_begin + sub, c_end);
-  const int nst = (w_end - w_begin + PST - 1) / PST;
+  // Work in super-tiles of PST keys. The NWS waves of the sequence's workgroups take about 80%
+  // of them statically (wave gw: super-tiles gw + k NWS for k < NS), the rest one at a time from
+  // the (sequence, KV head) tile counter, two super-tiles ahead. Waves that started late or sit
+  // on busier parts of the chip (XCDs start up to ~3 us apart and differ by ~10% in the
+  // bandwidth they get) then take fewer of the dynamic super-tiles.
+  const int T = (n + PST - 1) / PST;
+  const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * NWAVE;
+  const int gw = (x - plan.split_begin[b]) * NWAVE + wv;
+  const int NS = max(2, (4 * T) / (5 * NWS));  // static super-tiles per wave
   const int R = G * L;  // <= 4
-  // Fused append: the wave whose range holds row n - 1 (the sequence's new last row) quantizes
-  // the new K and V rows itself, patches them into its LDS copy of that super-tile (whatever the
-  // copy read from the cache row is replaced) and stores them to the cache at the end.
+  // Fused append: the wave that gets super-tile app_t (holding row n - 1, the sequence's new last
+  // row) patches the new K and V rows, quantized by every wave up front, into its LDS copy of that
+  // super-tile (whatever the copy read from the cache row is replaced) and stores them to the
+  // cache at the end.
   const int nrow = n - 1;
-  const bool app = args.knew != nullptr && w_begin <= nrow && nrow < w_end;  // wave-uniform
-  const int app_si = app ? (nrow - w_begin) / PST : -1;
-  const int app_r = app ? nrow - (w_begin + app_si * PST) : 0;
+  const bool app = args.knew != nullptr;
+  const int app_t = app ? nrow / PST : -1;
+  const int app_r = nrow - (nrow / PST) * PST;
   const int Hq = Hkv * G;
   const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
 
@@ -485,21 +489,23 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const uint32_t* vsw = reinterpret_cast<const uint32_t*>(vs + row0 * 2);
   const uint32_t* vbw = reinterpret_cast<const uint32_t*>(vb + row0 * 2);
   const int causal_bound = n - L + qi;  // query qi sees keys t <= causal_bound
+  const int last_row = n - 1;
+  const uint32_t ctr_off = (uint32_t)(TILE_CTR_BYTES + TILE_CTR_STRIDE * (b * Hkv + hk));
   PackTerms& tm = sm.loop.terms[wv];
 
   // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
   // bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the LDS row (the
   // swizzle read back in process). A full super-tile uses the scalar row base t0 and per-lane
-  // offsets that never change; the last one clamps rows to the wave's last key (past the end the
-  // copies land in the unused buffer and are never read).
+  // offsets that never change; the last one clamps rows to the sequence's last row, and so do
+  // super-tiles past the end (their copies land in a buffer that is never read).
   const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
   const uint32_t col_off = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
   uint32_t row_off[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
-  auto issue = [&](int si, auto bufc) {
+  auto issue = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
-    const int t0 = w_begin + si * PST;
+    const int t0 = tile * PST;
     const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(PackBuf));
     constexpr int OK = offsetof(PackBuf, k), OV = offsetof(PackBuf, v);
     constexpr int OKS = offsetof(PackBuf, ks), OKB = offsetof(PackBuf, kb);
@@ -508,7 +514,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const uint8_t* vb0 = vbase;
     const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
     uint32_t ro[8], wo;
-    if (t0 + PST <= w_end) {
+    if (t0 + PST <= n) {
       kb0 += (int64_t)t0 * D;
       vb0 += (int64_t)t0 * D;
       w0 += t0;
@@ -519,10 +525,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       for (int u = 0; u < 8; ++u) ro[u] = row_off[u];
       wo = 4u * (uint32_t)lane;
     } else {
-      const int last = max(w_end - 1, 0);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last) * D + col_off;
-      wo = 4u * (uint32_t)min(t0 + lane, last);
+      for (int u = 0; u < 8; ++u)
+        ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last_row) * D + col_off;
+      wo = 4u * (uint32_t)min(t0 + lane, last_row);
     }
     dma_b128<OK + 0>(kb0, ro[0], lb);
     dma_b128<OV + 0>(vb0, ro[0], lb);
@@ -552,9 +558,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const uint32_t sel_lo1 = mt == 2 ? ~0u : 0u, sel_hi1 = mt == 3 ? ~0u : 0u;
   const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
 
-  auto process = [&](int si, auto bufc) {
+  auto process = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
-    const int t0 = w_begin + si * PST;
+    const int t0 = tile * PST;
     const PackBuf& pb = sm.loop.buf[wv][BUF];
     // per-key terms, one lane per key: K scale * scale * log2(e) * 2^24, K bias, V scale, V bias
     {
@@ -597,13 +603,13 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const float ku0v[4] = {ku0.x, ku0.y, ku0.z, ku0.w}, ku1v[4] = {ku1.x, ku1.y, ku1.z, ku1.w};
     float sc[4];
     float tmax = -INFINITY;
-    const bool full = t0 + PST <= w_end && (!CAUSAL || t0 + PST - 1 <= n - L);
+    const bool full = t0 + PST <= n && (!CAUSAL || t0 + PST - 1 <= n - L);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = fmaf(ks0v[r], c0[r], fmaf(ks1v[r], c1[r], fmaf(ku1v[r], qsum[1], ku0v[r] * qsum[0])));
       if (!full) {
         const int t = t0 + k0 + r;
-        bool ok = t < w_end;
+        bool ok = t < n;
         if (CAUSAL) ok = ok && t <= causal_bound;
         v = ok ? v : -INFINITY;
       }
@@ -667,7 +673,37 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 
   const std::integral_constant<int, 0> B0;
   const std::integral_constant<int, 1> B1;
-  issue(0, B0);  // the first super-tile streams in while q is loaded and converted
+  // One tile-counter increment by lane 0 when `dyn` (exec narrowed to lane 0 inside the asm, or
+  // to no lane for a static step: the same instruction sequence every step, so that the waits
+  // below keep fixed counts), the old value in lane 0 of the returned VGPR. Inline asm like the
+  // copies, so that the compiler inserts no wait for it: `landed` reads it in the same statement
+  // as the explicit s_waitcnt that covers it (vector memory operations complete in issue order,
+  // and the grab precedes the 20 copies of the next super-tile).
+  auto grab = [&](bool dyn) {
+    uint32_t old;
+    uint64_t sv;
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(dyn ? 1u : 0u);
+    asm volatile("s_mov_b64 %1, exec\n\ts_mov_b32 exec_lo, %5\n\ts_mov_b32 exec_hi, 0\n\t"
+                 "global_atomic_add %0, %2, %3, %4 sc0\n\ts_mov_b64 exec, %1"
+                 : "=&v"(old), "=&s"(sv)
+                 : "v"(ctr_off), "v"(1u), "s"(args.counters), "s"(mask)
+                 : "memory");
+    return old;
+  };
+  // Waits for the current super-tile's copies and the grab issued after them; returns the index
+  // of the wave's super-tile number k2 (k2 > that of nxt): static below NS, else the grabbed
+  // value past the static ones. Clamped to (nxt, T] so that the loop always advances and every
+  // copy address stays inside the sequence.
+  auto landed = [&](uint32_t g, int k2, int nxt_tile) {
+    int v;
+    asm volatile("s_waitcnt vmcnt(20)\n\tv_readfirstlane_b32 %0, %1" : "=s"(v) : "v"(g) : "memory");
+    const int t = k2 < NS ? gw + k2 * NWS : NS * NWS + v;
+    return min(max(t, nxt_tile + 1), T);
+  };
+  int cur = min(gw, T), nxt = min(gw + NWS, T);  // wave-uniform super-tile indices
+  int k = 0;                                      // cur is the wave's super-tile number k
+  issue(cur, B0);  // the first super-tile streams in while q is loaded and converted
+  uint32_t grabbed = grab(2 >= NS);               // for super-tile number 2
 
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
   {
@@ -692,6 +728,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   }
   QPair app_k = {0u, 0, 0}, app_v = {0u, 0, 0};
   uint32_t app_w[4] = {0u, 0u, 0u, 0u};  // ks, kb, vs, vb words of the new row (group 0 low)
+  bool patched = false;
   if (app) {
     const int64_t src = ((int64_t)b * Hkv + hk) * D + 2 * lane;
     app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(args.knew + src));
@@ -718,25 +755,40 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     }
   };
 
-  // Unrolled by two so that each buffer's LDS offsets are constants. Super-tile si + 1 is always
-  // issued before si is processed (past the last super-tile the copies clamp to the wave's last
-  // row and are never read), so the wait is a fixed count: the 20 copies issued after si's.
-  for (int si = 0; si < nst; si += 2) {
+  // Unrolled by two so that each buffer's LDS offsets are constants. The next super-tile is
+  // always issued before the current one is processed (past the end the copies clamp to the last
+  // row and are never read), so the wait is a fixed count: the 20 copies issued after the current
+  // super-tile's copies and the grab between them.
+  for (;;) {
+    if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
-    issue(si + 1, B1);
-    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile si has landed in LDS
-    if (si == app_si) patch(B0);
-    process(si, B0);
-    if (si + 1 < nst) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(si + 2, B0);
-      asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
-      if (si + 1 == app_si) patch(B1);
-      process(si + 1, B1);
+    issue(nxt, B1);
+    int after = landed(grabbed, k + 2, nxt);  // super-tile cur and the grab have landed
+    grabbed = grab(k + 3 >= NS);
+    if (cur == app_t) {
+      patch(B0);
+      patched = true;
     }
+    process(cur, B0);
+    cur = nxt;
+    nxt = after;
+    ++k;
+    if (cur >= T) break;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(nxt, B0);
+    after = landed(grabbed, k + 2, nxt);
+    grabbed = grab(k + 3 >= NS);
+    if (cur == app_t) {
+      patch(B1);
+      patched = true;
+    }
+    process(cur, B1);
+    cur = nxt;
+    nxt = after;
+    ++k;
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (app) {  // the new row goes to the cache (no copy in this kernel reads it back)
+  if (patched) {  // the new row goes to the cache (no copy in this kernel reads it back)
     const int64_t crow = row0 + nrow;
     *reinterpret_cast<uint16_t*>(args.kc + crow * D + 2 * lane) = (uint16_t)app_k.codes;
     *reinterpret_cast<uint16_t*>(args.vc + crow * D + 2 * lane) = (uint16_t)app_v.codes;

@@ -27,8 +27,8 @@ _workspaces: dict = {}
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per-(device, stream) attention workspace, grown on demand. Calls on one stream are ordered,
     so reuse is safe; different streams get different buffers. A new buffer starts zeroed: its
-    first LQ_WS_ZERO_BYTES bytes are the kernels' arrival counters, which every call leaves at
-    zero, so only attention calls may use it."""
+    first LQ_WS_ZERO_BYTES bytes are the kernels' arrival and tile counters, which every call
+    leaves at zero, so only attention calls may use it."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
