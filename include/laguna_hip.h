@@ -41,7 +41,7 @@ extern "C" {
  * every call leaves them zero again. Calls that share a workspace must be ordered (one stream).
  * At most 2048 (sequence, KV head) pairs per call.
  */
-#define LQ_WS_ZERO_BYTES 139264
+#define LQ_WS_ZERO_BYTES 131072
 
 /* Library version (major*10000 + minor*100 + patch). */
 int lq_version(void);

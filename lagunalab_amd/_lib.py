@@ -17,7 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "liblaguna_hip.so"
 LQ_OK, LQ_EINVAL, LQ_EHIP, LQ_EWORKSPACE = 0, 1, 2, 3
 LQ_KV_Q8, LQ_KV_Q4, LQ_KV_BF16 = 8, 4, 16
 LQ_MAX_SEQS = 64
-LQ_WS_ZERO_BYTES = 139264  # leading workspace bytes that attention calls keep at zero
+LQ_WS_ZERO_BYTES = 131072  # leading workspace bytes that attention calls keep at zero
 
 i64, i32, f32, vp = C.c_int64, C.c_int, C.c_float, C.c_void_p
 

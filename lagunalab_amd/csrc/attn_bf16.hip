@@ -34,9 +34,9 @@ struct Bf16Buf {
 struct Bf16Smem {
   union {
     Bf16Buf buf[BW][2];
-    float acc[BW][4][D];
+    alignas(16) float acc[BW][4][D];
   };
-  float st[BW][4][6];
+  alignas(16) float st[BW][4][6];
 };
 
 __device__ __forceinline__ bf16x8_t u4_as_bf8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }

@@ -211,18 +211,37 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 
 // Epilogue of the packed kernels. Per wave: the accumulator columns of the 4 key tiles of each
 // query row are summed (lanes 4 and 8 apart in a row), the softmax sum and the two bias sums over
-// all lanes; then the NW waves meet in LDS (acc_lds [NW][4][D], st_lds [NW][4][6]) and their
-// log-sum-exp merge is the workgroup's split partial: acc * out_scale + bias sum of the quant
-// group, written with agent-scope stores. Then the arrival count, and the last workgroup of the
+// all lanes; then the NW waves meet in LDS and their log-sum-exp merge is the workgroup's split
+// partial: acc * out_scale + bias sum of the quant group, written with agent-scope stores. The
+// LDS layout puts the NW waves' values of one quantity side by side (acc_lds [4][D][NW],
+// st_lds [4][4][NW]: m, l, bias sum 0, bias sum 1), so that each output element takes three
+// NW-wide LDS reads issued together. Then the arrival count, and the last workgroup of the
 // (sequence, KV head) merges all splits (merge_rows4). The caller has synchronised the workgroup
-// so that acc_lds/st_lds may overwrite its tile buffers.
+// so that acc_lds/st_lds (16-byte aligned, at least 4 D NW and 16 NW floats) may overwrite its
+// tile buffers.
 // EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (row) + p (the 4-bit kernel's P.V
 // operands); otherwise tile j holds dims 16 j + row.
+template <int NW>
+struct WaveVec;
+template <>
+struct WaveVec<4> {
+  typedef float4 T;
+  static __device__ __forceinline__ float get(const float4& v, int w) {
+    return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+  }
+};
+template <>
+struct WaveVec<2> {
+  typedef float2 T;
+  static __device__ __forceinline__ float get(const float2& v, int w) { return w == 0 ? v.x : v.y; }
+};
+
 template <int NW, bool EVEN_ODD = false>
 __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bsum0, float bsum1,
                               float out_scale, float* acc_lds, float* st_lds, int* sh_last,
                               const AttnArgs& args, const DecodePlan& plan, int x, int b, int hk,
                               int R) {
+  typedef typename WaveVec<NW>::T wvec;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -254,14 +273,13 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int dim = EVEN_ODD ? 32 * (dt >> 1) + 2 * (4 * lq4 + r) + (dt & 1) : 16 * dt + 4 * lq4 + r;
-        acc_lds[(wv * 4 + lc) * D + dim] = oacc[dt][r];
+        acc_lds[(lc * D + dim) * NW + wv] = oacc[dt][r];
       }
     if (lq4 == 0) {
-      float* st = st_lds + (wv * 4 + lc) * 6;
-      st[0] = m_run;
-      st[1] = tot[0];
-      st[2] = tot[1];
-      st[3] = tot[2];
+      st_lds[(lc * 4 + 0) * NW + wv] = m_run;
+      st_lds[(lc * 4 + 1) * NW + wv] = tot[0];
+      st_lds[(lc * 4 + 2) * NW + wv] = tot[1];
+      st_lds[(lc * 4 + 3) * NW + wv] = tot[2];
     }
   }
   __syncthreads();
@@ -269,33 +287,38 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     const int col = o / D;
     const int d = o - col * D;
     const int g = d >> 6;
+    const wvec m = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 0) * NW);
+    const wvec bs = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 2 + g) * NW);
+    const wvec ac = *reinterpret_cast<const wvec*>(acc_lds + (col * D + d) * NW);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, st_lds[(w * 4 + col) * 6]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
     float a = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float* st = st_lds + (w * 4 + col) * 6;
-      const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
-      a += e * fmaf(acc_lds[(w * 4 + col) * D + d], out_scale, st[2 + g]);
+      const float mw = WaveVec<NW>::get(m, w);
+      const float e = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+      a += e * fmaf(WaveVec<NW>::get(ac, w), out_scale, WaveVec<NW>::get(bs, w));
     }
     st_agent(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
   }
   if (tid < R) {
     const int col = tid;
+    const wvec m = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 0) * NW);
+    const wvec l = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 1) * NW);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, st_lds[(w * 4 + col) * 6]);
-    float l = 0.0f;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
+    float lt = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float* st = st_lds + (w * 4 + col) * 6;
-      l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
+      const float mw = WaveVec<NW>::get(m, w);
+      lt += mw == -INFINITY ? 0.0f : exp2f(mw - M) * WaveVec<NW>::get(l, w);
     }
     float* pml =
         reinterpret_cast<float*>(args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col);
     st_agent(pml, M);
-    st_agent(pml + 1, l);
+    st_agent(pml + 1, lt);
   }
 
   // ---- split merge, fused: the last workgroup of (sequence, KV head) to store its partials
@@ -307,15 +330,13 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    uint32_t* c = args.counters + b * Hkv + hk;
+    uint32_t* c = arrival_counter(args.counters, b * Hkv + hk);
     const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
     const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev + 1 == ns;
     if (last) {  // every workgroup of (b, hk) is past its loop: reset both counters
-      uint32_t* tc = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(args.counters) +
-                                                 TILE_CTR_BYTES + TILE_CTR_STRIDE * (b * Hkv + hk));
       __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(tc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(c + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     *sh_last = last;
   }

@@ -45,8 +45,8 @@ struct Q4Smem {
       Q4Terms terms[QW];
     } loop;
     struct {
-      float acc[QW][4][D];
-      float st[QW][4][6];
+      alignas(16) float acc[QW][4][D];
+      alignas(16) float st[QW][4][6];
       int last;
     } fin;
   };

@@ -49,17 +49,18 @@ struct AttnArgs {
 
 typedef void (*QAttnFn)(AttnArgs, DecodePlan);
 
-// Workspace of the attention calls: per sequence and KV head i an arrival counter (uint32 at
-// 4 i) and a tile counter of the packed kernels (uint32 at TILE_CTR_BYTES + TILE_CTR_STRIDE i,
-// one per 64-byte line: atomics on one line serialize), both zero between calls (each call's
-// last arrival resets them), then the split partials. The counter area has a fixed size so that
-// calls of any shape can share a workspace.
+// Workspace of the attention calls: per sequence and KV head i one 64-byte line of counters
+// (atomics on one line serialize at ~10 ns each, so every pair gets its own): the workgroups'
+// arrival count (uint32 at CTR_STRIDE i) and the packed kernels' tile count (at CTR_STRIDE i +
+// 4), both zero between calls (each call's last arrival resets them), then the split partials.
+// The counter area has a fixed size so that calls of any shape can share a workspace.
 constexpr int64_t WS_COUNTER_BYTES = LQ_WS_ZERO_BYTES;
 constexpr int64_t MAX_COUNTERS = 2048;
-constexpr int TILE_CTR_BYTES = 4 * MAX_COUNTERS;
-constexpr int TILE_CTR_STRIDE = 64;
-static_assert(TILE_CTR_BYTES + TILE_CTR_STRIDE * MAX_COUNTERS <= WS_COUNTER_BYTES,
-              "counter area too small");
+constexpr int CTR_STRIDE = 64;
+static_assert(CTR_STRIDE * MAX_COUNTERS <= WS_COUNTER_BYTES, "counter area too small");
+__host__ __device__ inline uint32_t* arrival_counter(uint32_t* counters, int i) {
+  return reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(counters) + CTR_STRIDE * i);
+}
 
 // MFMA attention kernel for `nt` 16-column tiles of query rows (G * L <= 16 * nt), causal for
 // multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4, which also merges

@@ -417,9 +417,9 @@ struct PackSmem {
       PackBuf buf[NWAVE][2];
       PackTerms terms[NWAVE];
     } loop;
-    float acc[NWAVE][4][D];  // wave partials, final merge
+    alignas(16) float acc[NWAVE][4][D];  // wave partials, final merge
   };
-  float st[NWAVE][4][6];
+  alignas(16) float st[NWAVE][4][6];
 };
 
 template <bool CAUSAL>
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const uint32_t* vbw = reinterpret_cast<const uint32_t*>(vb + row0 * 2);
   const int causal_bound = n - L + qi;  // query qi sees keys t <= causal_bound
   const int last_row = n - 1;
-  const uint32_t ctr_off = (uint32_t)(TILE_CTR_BYTES + TILE_CTR_STRIDE * (b * Hkv + hk));
+  const uint32_t ctr_off = (uint32_t)(CTR_STRIDE * (b * Hkv + hk) + 4);  // tile counter
   PackTerms& tm = sm.loop.terms[wv];
 
   // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
@@ -677,8 +677,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   // to no lane for a static step: the same instruction sequence every step, so that the waits
   // below keep fixed counts), the old value in lane 0 of the returned VGPR. Inline asm like the
   // copies, so that the compiler inserts no wait for it: `landed` reads it in the same statement
-  // as the explicit s_waitcnt that covers it (vector memory operations complete in issue order,
-  // and the grab precedes the 20 copies of the next super-tile).
+  // as the explicit s_waitcnt that covers it (vector memory operations complete in issue order;
+  // each step issues the grab, then the 20 copies of the next super-tile, then waits until only
+  // those 20 are outstanding).
   auto grab = [&](bool dyn) {
     uint32_t old;
     uint64_t sv;
@@ -690,10 +691,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
                  : "memory");
     return old;
   };
-  // Waits for the current super-tile's copies and the grab issued after them; returns the index
-  // of the wave's super-tile number k2 (k2 > that of nxt): static below NS, else the grabbed
-  // value past the static ones. Clamped to (nxt, T] so that the loop always advances and every
-  // copy address stays inside the sequence.
+  // Waits for the current super-tile's copies and the grab issued after them (before the next
+  // super-tile's copies); returns the index of the wave's super-tile number k2 (that after nxt):
+  // static below NS, else the grabbed value past the static ones, clamped to (nxt, T] so that the
+  // loop always advances and every copy address stays inside the sequence.
   auto landed = [&](uint32_t g, int k2, int nxt_tile) {
     int v;
     asm volatile("s_waitcnt vmcnt(20)\n\tv_readfirstlane_b32 %0, %1" : "=s"(v) : "v"(g) : "memory");
@@ -703,7 +704,6 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   int cur = min(gw, T), nxt = min(gw + NWS, T);  // wave-uniform super-tile indices
   int k = 0;                                      // cur is the wave's super-tile number k
   issue(cur, B0);  // the first super-tile streams in while q is loaded and converted
-  uint32_t grabbed = grab(2 >= NS);               // for super-tile number 2
 
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
   {
@@ -757,14 +757,14 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 
   // Unrolled by two so that each buffer's LDS offsets are constants. The next super-tile is
   // always issued before the current one is processed (past the end the copies clamp to the last
-  // row and are never read), so the wait is a fixed count: the 20 copies issued after the current
-  // super-tile's copies and the grab between them.
+  // row and are never read), so the wait is a fixed count: the 20 copies of the next super-tile,
+  // issued after the current one's copies and after the grab of the one after next.
   for (;;) {
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
+    uint32_t grabbed = grab(k + 2 >= NS);
     issue(nxt, B1);
     int after = landed(grabbed, k + 2, nxt);  // super-tile cur and the grab have landed
-    grabbed = grab(k + 3 >= NS);
     if (cur == app_t) {
       patch(B0);
       patched = true;
@@ -775,9 +775,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     ++k;
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    grabbed = grab(k + 2 >= NS);
     issue(nxt, B0);
     after = landed(grabbed, k + 2, nxt);
-    grabbed = grab(k + 3 >= NS);
     if (cur == app_t) {
       patch(B1);
       patched = true;
