@@ -1,0 +1,457 @@
+// Attention over the 8-bit KV cache for more than 4 query rows per KV head: the causal verify
+// block of speculative decoding (G * L rows, L <= 16) and single-token decode with G > 4.
+//
+// Replaces, for verify blocks, the reference's unfused path (dequantize, laguna_mlx/cache.py:
+// 99-100, then SDPA with the bottom-right causal mask, laguna.py:107, 183-186), and for decode
+// q8_decode_attention (laguna_mlx/q8_attn.py:102-130) when G > 4.
+//
+// Dense MFMA layout (v_mfma_f32_16x16x32_f16): the 16 columns of an N tile are 16 query rows, so
+// NT tiles serve up to 16 NT rows; the 16 rows of an M tile are 16 keys; a super-tile of 64 keys
+// is 4 M tiles.
+//  * Q.K^T per (M tile mt, quant group g, N tile nt): two MFMAs over the 64 dims of group g. A
+//    lane of lane group q supplies dims 64 g + 16 q + 8 e + (0..7) of key 16 mt + (lane % 16) for
+//    k-step e (one 16-byte LDS read per (mt, g)); codes enter the MFMA as fp16 subnormals
+//    c * 2^-24 (one v_perm_b32 per two codes, exact), 2^24 folded into the K scale.
+//  * The affine terms fold out per key and group: q.(s c + b) = s (q.c) + b sum_g(q); the per-key
+//    terms (scaled K scale, K bias, V scale, V bias) are computed once per super-tile by one lane
+//    per key and shared through LDS.
+//  * After Q.K^T a lane holds, per N tile, the scores of keys 16 mt + 4 q + r (r < 4) of one
+//    query row; softmax runs in that layout (row max: in-lane over mt and r, then over the 4
+//    lane groups), with lazy rescaling and exp2 of scores pre-scaled by scale * log2(e).
+//  * P.V: two k-steps of 32 keys (M tiles 2e and 2e+1); A = V^T (16 dims x 32 keys) from one
+//    transposed 8-byte LDS read (ds_read_b64_tr_b8), B = P * V scale in fp16 built from the
+//    lane's own weights (k-slot j of lane group q = key 16 (2e + j / 4) + 4 q + j % 4).
+//  * Work: the waves of a sequence's workgroups take super-tiles gw, gw + NWS, ... (static,
+//    interleaved); K, V and the word arrays of a super-tile go global -> LDS with 20 DMA copies,
+//    double-buffered per wave, one fixed wait per super-tile.
+//  * Partials (m, l, acc) per (workgroup, query row) go to the workspace; decode_merge_kernel
+//    merges them (at 16+ rows per KV head the partials of 32 workgroups are ~330 KB per head, too
+//    much for one workgroup to merge at the end of the attention kernel).
+#include "attn_dev.h"
+
+namespace lq {
+namespace {
+
+using namespace attn;
+
+constexpr int DST = 64;  // keys per super-tile
+constexpr int DW = 4;    // waves per workgroup
+
+struct DenseBuf {
+  uint8_t k[DST * D];
+  uint8_t v[DST * D];
+  uint32_t ks[DST];
+  uint32_t kb[DST];
+  uint32_t vs[DST];
+  uint32_t vb[DST];
+};
+
+struct DenseTerms {  // per key of the current super-tile
+  float ks0[DST], ks1[DST], ku0[DST], ku1[DST];  // s_g * scale*log2e * 2^24, b_g
+  float vs0[DST], vs1[DST], vb0[DST], vb1[DST];
+};
+
+template <int NT>
+struct DenseSmem {
+  union {
+    struct {
+      DenseBuf buf[DW][2];
+      DenseTerms terms[DW];
+    } loop;
+    alignas(16) float acc[DW][16 * NT][D];  // wave partials (epilogue)
+  };
+  alignas(16) float st[DW][16 * NT][4];  // m, l, bias sum 0, bias sum 1
+};
+
+template <int NT, bool CAUSAL>
+__global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, DecodePlan plan) {
+  __shared__ DenseSmem<NT> sm;
+  const uint16_t* __restrict__ q = args.q;
+  const int Hkv = args.Hkv, G = args.G, L = args.L;
+  const int64_t cap = args.cap;
+  const float qk_scale_log2 = args.qk_scale_log2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+  const int x = blockIdx.x;
+  const int hk = blockIdx.y;
+  int b;
+  find_seq(plan, x, b);
+  const int n = plan.len[b];
+  const int T = (n + DST - 1) / DST;
+  const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * DW;
+  const int gw = (x - plan.split_begin[b]) * DW + wv;
+  const int R = G * L;  // query rows of this KV head, <= 16 NT
+  const int Hq = Hkv * G;
+  const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
+  const int last_row = n - 1;
+
+  const int lc = lane & 15;
+  const int lq4 = lane >> 4;
+
+  // ---- B operands of Q.K^T: per N tile, group g, k-step e: q[row 16 nt + lc] dims
+  // 64 g + 16 lq4 + 8 e + (0..7), fp16; qsum: the group's sum of those fp16 values (all lanes
+  // of the column), times scale * log2(e).
+  half8_t qb[NT][2][2];
+  float qsum[NT][2];
+  int qpos[NT];  // position i of the query row in its block (causal bound)
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int qr_i = 16 * nt + lc;
+    const bool valid = qr_i < R;
+    const int gh = valid ? qr_i / L : 0;
+    const int i = valid ? qr_i - gh * L : 0;
+    qpos[nt] = i;
+    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + i) * D;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float s = 0.0f;
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4);
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4 + 8);
+      const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t wd = w[4 * e + j];
+          const _Float16 lo = valid ? (_Float16)bf16_lo(wd) : (_Float16)0.0f;
+          const _Float16 hi = valid ? (_Float16)bf16_hi(wd) : (_Float16)0.0f;
+          qb[nt][g][e][2 * j] = lo;
+          qb[nt][g][e][2 * j + 1] = hi;
+          s += (float)lo + (float)hi;
+        }
+      s += shfl_xor_f(s, 16);
+      s += shfl_xor_f(s, 32);
+      qsum[nt][g] = s * qk_scale_log2;
+    }
+  }
+
+  f4_t oacc[NT][8];  // out^T[16 dt + 4 lq4 + r][row 16 nt + lc]
+  float m_run[NT], lsum[NT], bsum[NT][2];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[nt] = -INFINITY;
+    lsum[nt] = 0.0f;
+    bsum[nt][0] = bsum[nt][1] = 0.0f;
+  }
+
+  const uint8_t* kbase = args.kc + row0 * D;
+  const uint8_t* vbase = args.vc + row0 * D;
+  const uint32_t* ksw = reinterpret_cast<const uint32_t*>(args.ks + row0 * 2);
+  const uint32_t* kbw = reinterpret_cast<const uint32_t*>(args.kb + row0 * 2);
+  const uint32_t* vsw = reinterpret_cast<const uint32_t*>(args.vs + row0 * 2);
+  const uint32_t* vbw = reinterpret_cast<const uint32_t*>(args.vb + row0 * 2);
+  const int causal_base = n - L;  // query i sees keys t <= causal_base + i
+  DenseTerms& tm = sm.loop.terms[wv];
+
+  // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
+  // bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the LDS row. A
+  // full super-tile uses the scalar row base t0 and per-lane offsets that never change; the last
+  // one clamps rows to the sequence's last row, and so do super-tiles past the end (their copies
+  // land in a buffer that is never read).
+  const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
+  const uint32_t col_off = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
+  uint32_t row_off[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
+  auto issue = [&](int tile, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const int t0 = tile * DST;
+    const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(DenseBuf));
+    constexpr int OK = offsetof(DenseBuf, k), OV = offsetof(DenseBuf, v);
+    constexpr int OKS = offsetof(DenseBuf, ks), OKB = offsetof(DenseBuf, kb);
+    constexpr int OVS = offsetof(DenseBuf, vs), OVB = offsetof(DenseBuf, vb);
+    const uint8_t* kb0 = kbase;
+    const uint8_t* vb0 = vbase;
+    const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
+    uint32_t ro[8], wo;
+    if (t0 + DST <= n) {
+      kb0 += (int64_t)t0 * D;
+      vb0 += (int64_t)t0 * D;
+      w0 += t0;
+      w1 += t0;
+      w2 += t0;
+      w3 += t0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) ro[u] = row_off[u];
+      wo = 4u * (uint32_t)lane;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last_row) * D + col_off;
+      wo = 4u * (uint32_t)min(t0 + lane, last_row);
+    }
+    dma_b128<OK + 0>(kb0, ro[0], lb);
+    dma_b128<OV + 0>(vb0, ro[0], lb);
+    dma_b128<OK + 1024>(kb0, ro[1], lb);
+    dma_b128<OV + 1024>(vb0, ro[1], lb);
+    dma_b128<OK + 2048>(kb0, ro[2], lb);
+    dma_b128<OV + 2048>(vb0, ro[2], lb);
+    dma_b128<OK + 3072>(kb0, ro[3], lb);
+    dma_b128<OV + 3072>(vb0, ro[3], lb);
+    dma_b128<OK + 4096>(kb0, ro[4], lb);
+    dma_b128<OV + 4096>(vb0, ro[4], lb);
+    dma_b128<OK + 5120>(kb0, ro[5], lb);
+    dma_b128<OV + 5120>(vb0, ro[5], lb);
+    dma_b128<OK + 6144>(kb0, ro[6], lb);
+    dma_b128<OV + 6144>(vb0, ro[6], lb);
+    dma_b128<OK + 7168>(kb0, ro[7], lb);
+    dma_b128<OV + 7168>(vb0, ro[7], lb);
+    dma_b32<OKS>(w0, wo, lb);
+    dma_b32<OKB>(w1, wo, lb);
+    dma_b32<OVS>(w2, wo, lb);
+    dma_b32<OVB>(w3, wo, lb);
+  };
+
+  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+
+  auto process = [&](int tile, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const int t0 = tile * DST;
+    const DenseBuf& pb = sm.loop.buf[wv][BUF];
+    {  // per-key terms, one lane per key
+      const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
+      tm.ks0[lane] = bf16_lo(a) * kscale;
+      tm.ks1[lane] = bf16_hi(a) * kscale;
+      tm.ku0[lane] = bf16_lo(c);
+      tm.ku1[lane] = bf16_hi(c);
+      tm.vs0[lane] = bf16_lo(e);
+      tm.vs1[lane] = bf16_hi(e);
+      tm.vb0[lane] = bf16_lo(f);
+      tm.vb1[lane] = bf16_hi(f);
+    }
+    // Q.K^T: c[mt][nt][g]
+    f4_t c[4][NT][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int r = 16 * mt + lc;
+      const uint8_t* kr = pb.k + r * D;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const uint4 u = *reinterpret_cast<const uint4*>(kr + 16 * ((4 * g + lq4) ^ (r & 7)));
+        const half8_t a0 = codes8_sub(u.x, u.y);
+        const half8_t a1 = codes8_sub(u.z, u.w);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          f4_t z = {0.f, 0.f, 0.f, 0.f};
+          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qb[nt][g][0], z, 0, 0, 0);
+          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qb[nt][g][1], z, 0, 0, 0);
+          c[mt][nt][g] = z;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool full = t0 + DST <= n && (!CAUSAL || t0 + DST - 1 <= causal_base);
+    // scores of this lane's keys 16 mt + 4 lq4 + r, per N tile (per-key terms read per M tile)
+    float sc[NT][4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int k0 = 16 * mt + 4 * lq4;
+      const float4 s0 = *reinterpret_cast<const float4*>(tm.ks0 + k0);
+      const float4 s1 = *reinterpret_cast<const float4*>(tm.ks1 + k0);
+      const float4 u0 = *reinterpret_cast<const float4*>(tm.ku0 + k0);
+      const float4 u1 = *reinterpret_cast<const float4*>(tm.ku1 + k0);
+      const float s0v[4] = {s0.x, s0.y, s0.z, s0.w}, s1v[4] = {s1.x, s1.y, s1.z, s1.w};
+      const float u0v[4] = {u0.x, u0.y, u0.z, u0.w}, u1v[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = fmaf(s0v[r], c[mt][nt][0][r],
+                         fmaf(s1v[r], c[mt][nt][1][r],
+                              fmaf(u1v[r], qsum[nt][1], u0v[r] * qsum[nt][0])));
+          if (!full) {
+            const int t = t0 + k0 + r;
+            bool ok = t < n;
+            if (CAUSAL) ok = ok && t <= causal_base + qpos[nt];
+            v = ok ? v : -INFINITY;
+          }
+          sc[nt][mt][r] = v;
+        }
+    }
+    uint32_t pw[NT][2][2][4];  // P.V B operands: [nt][k-step e][group][dword]
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[nt][mt][r]);
+      tmax = max_xor16(tmax);
+      tmax = max_xor32(tmax);
+      const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
+      if (__builtin_amdgcn_ballot_w64(bump)) {
+        const float mn = bump ? tmax : m_run[nt];
+        const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2f(m_run[nt] - mn);
+        m_run[nt] = mn;
+        lsum[nt] *= alpha;
+        bsum[nt][0] *= alpha;
+        bsum[nt][1] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+      }
+      const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+      float ls = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float w0[8], w1[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int mt = 2 * e + h;
+          const int k0 = 16 * mt + 4 * lq4;
+          const float4 vs0 = *reinterpret_cast<const float4*>(tm.vs0 + k0);
+          const float4 vs1 = *reinterpret_cast<const float4*>(tm.vs1 + k0);
+          const float4 vb0 = *reinterpret_cast<const float4*>(tm.vb0 + k0);
+          const float4 vb1 = *reinterpret_cast<const float4*>(tm.vb1 + k0);
+          const float vs0v[4] = {vs0.x, vs0.y, vs0.z, vs0.w}, vs1v[4] = {vs1.x, vs1.y, vs1.z, vs1.w};
+          const float vb0v[4] = {vb0.x, vb0.y, vb0.z, vb0.w}, vb1v[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(sc[nt][mt][r] - mref);
+            ls += p;
+            b0 = fmaf(p, vb0v[r], b0);
+            b1 = fmaf(p, vb1v[r], b1);
+            w0[4 * h + r] = p * vs0v[r];
+            w1[4 * h + r] = p * vs1v[r];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pw[nt][e][0][j] = pack_h2(w0[2 * j], w0[2 * j + 1]);
+          pw[nt][e][1][j] = pack_h2(w1[2 * j], w1[2 * j + 1]);
+        }
+      }
+      lsum[nt] += ls;
+      bsum[nt][0] += b0;
+      bsum[nt][1] += b1;
+    }
+    // P.V: A = V^T tile (16 dims x 32 keys) via one transposed LDS read per dim tile. Source
+    // lane s of each 16-lane group addresses key T[s/2] at column offset 8 (s % 2), so result
+    // lane i receives keys T[0..7] of dim i.
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int kslot = lc >> 1;
+      const int key = 32 * e + (kslot < 4 ? 4 * lq4 + kslot : 16 + 4 * lq4 + (kslot - 4));
+      const uint8_t* vrow = pb.v + key * D + 8 * (lc & 1);
+      const int sw = key & 7;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const v2i_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (dt ^ sw)));
+        const half8_t a = codes8_sub((uint32_t)raw.x, (uint32_t)raw.y);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const uint32_t* w = pw[nt][e][dt >> 2];
+          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, words_as_h8(w[0], w[1], w[2], w[3]),
+                                                                oacc[nt][dt], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  const std::integral_constant<int, 0> B0;
+  const std::integral_constant<int, 1> B1;
+  // Unrolled by two so that each buffer's LDS offsets are constants. The next super-tile is
+  // always issued before the current one is processed (past the end the copies clamp to the last
+  // row and are never read), so the wait is a fixed count: the 20 copies issued after it.
+  int cur = min(gw, T);
+  issue(cur, B0);
+  for (;;) {
+    if (cur >= T) break;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
+    issue(min(cur + NWS, T), B1);
+    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile cur has landed in LDS
+    process(cur, B0);
+    cur = min(cur + NWS, T);
+    if (cur >= T) break;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(min(cur + NWS, T), B0);
+    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    process(cur, B1);
+    cur = min(cur + NWS, T);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- per-wave totals over the 4 lane groups that share a column
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    lsum[nt] = sum_xor32(sum_xor16(lsum[nt]));
+    bsum[nt][0] = sum_xor32(sum_xor16(bsum[nt][0]));
+    bsum[nt][1] = sum_xor32(sum_xor16(bsum[nt][1]));
+  }
+  __syncthreads();  // every wave is done with its LDS tiles before they are reused below
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int col = nt * 16 + lc;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.acc[wv][col][16 * dt + 4 * lq4 + r] = oacc[nt][dt][r];
+    if (lq4 == 0) {
+      float* st = sm.st[wv][col];
+      st[0] = m_run[nt];
+      st[1] = lsum[nt];
+      st[2] = bsum[nt][0];
+      st[3] = bsum[nt][1];
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the waves (log-sum-exp) into the workgroup's partial
+  for (int o = tid; o < R * D; o += 64 * DW) {
+    const int col = o / D;
+    const int d = o - col * D;
+    const int g = d >> 6;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) {
+      const float* st = sm.st[w][col];
+      const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
+      a += e * fmaf(sm.acc[w][col][d], 16777216.0f, st[2 + g]);
+    }
+    args.part_acc[((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d] = a;
+  }
+  if (tid < R) {
+    const int col = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) {
+      const float* st = sm.st[w][col];
+      l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
+    }
+    args.part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
+  }
+}
+
+}  // namespace
+
+QAttnFn q8_dense_attn_fn(int nt, bool causal) {
+  if (causal) {
+    switch (nt) {
+      case 1: return q8_attn_dense_kernel<1, true>;
+      case 2: return q8_attn_dense_kernel<2, true>;
+      case 3: return q8_attn_dense_kernel<3, true>;
+      case 4: return q8_attn_dense_kernel<4, true>;
+    }
+  } else {
+    switch (nt) {
+      case 1: return q8_attn_dense_kernel<1, false>;
+      case 2: return q8_attn_dense_kernel<2, false>;
+      case 3: return q8_attn_dense_kernel<3, false>;
+      case 4: return q8_attn_dense_kernel<4, false>;
+    }
+  }
+  return nullptr;
+}
+
+}  // namespace lq

@@ -104,16 +104,6 @@ __device__ __forceinline__ uint32_t affine_code(float x, AffineParams p) {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-// Two codes c0 (byte sel0) and c1 (byte sel1) of `w` as the fp16 pair (1024 + c0, 1024 + c1):
-// 0x64XX is the fp16 number 1024 + XX for XX in [0, 255]. One v_perm_b32. `sel` selects the
-// bytes of `w` for result bytes 0 and 2; bytes 1 and 3 come from the constant 0x64646464.
-__device__ __forceinline__ half2_t codes_as_h2(uint32_t w, uint32_t sel) {
-  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
-}
-// selectors for codes_as_h2: bytes (0,1) and (2,3) of w
-constexpr uint32_t SEL_B01 = 0x04010400u;
-constexpr uint32_t SEL_B23 = 0x04030402u;
-
 // Two codes of w as fp16 subnormals (bit pattern 0x00cc = c * 2^-24, exact): bytes (0,1) or (2,3).
 __device__ __forceinline__ uint32_t codes_sub_w(uint32_t w, uint32_t sel) {
   return __builtin_amdgcn_perm(0u, w, sel);
@@ -124,9 +114,6 @@ constexpr uint32_t SUB_B23 = 0x0c030c02u;
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
-  return __builtin_amdgcn_fdot2(a, b, c, false);
-}
 
 // ---------------------------------------------------------------------------------------------
 // device: wave64 cross-lane helpers

@@ -146,8 +146,8 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
                   int64_t& ws_bytes) {
   const int64_t R = (Hq / Hkv) * L;
   if (kind == LQ_KV_Q8) {
-    const int nt = attn_merges_itself(R) ? 0 : (int)((R + 15) / 16);  // 0: the packed kernel
-    k = {q8_attn_fn(nt, L > 1), 256};
+    const int nt = (int)((R + 15) / 16);
+    k = {attn_merges_itself(R) ? q8_attn_fn(L > 1) : q8_dense_attn_fn(nt, L > 1), 256};
   } else if (kind == LQ_KV_BF16 && R <= 4) {
     k = {bf16_attn_fn(L > 1), 128};
   } else if (kind == LQ_KV_Q4 && R <= 4) {

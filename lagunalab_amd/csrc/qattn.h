@@ -62,10 +62,12 @@ __host__ __device__ inline uint32_t* arrival_counter(uint32_t* counters, int i) 
   return reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(counters) + CTR_STRIDE * i);
 }
 
-// MFMA attention kernel for `nt` 16-column tiles of query rows (G * L <= 16 * nt), causal for
-// multi-row verify blocks; nt == 0 selects the packed kernel for G * L <= 4, which also merges
-// the splits (no decode_merge_kernel launch).
-QAttnFn q8_attn_fn(int nt, bool causal);
+// Packed 8-bit kernel (qattn.hip) for G * L <= 4 query rows per KV head, causal for multi-row
+// verify blocks; it also merges the splits (no decode_merge_kernel launch).
+QAttnFn q8_attn_fn(bool causal);
+// Dense-layout kernel (attn_dense.hip) for 4 < G * L <= 16 nt rows per KV head; partials merged
+// by decode_merge_kernel.
+QAttnFn q8_dense_attn_fn(int nt, bool causal);
 
 // The attention kernel for one call: its function and workgroup size.
 struct AttnKernel {

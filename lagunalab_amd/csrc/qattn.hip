@@ -1,31 +1,10 @@
-// Fused attention over the 8-bit KV cache on MFMA: single-token decode and the multi-query
-// causal verify block of speculative decoding.
+// Fused attention over the 8-bit KV cache on MFMA for at most 4 query rows per KV head:
+// single-token decode with G <= 4 and small causal verify blocks (G * L <= 4). Larger blocks take
+// the dense-layout kernel (attn_dense.hip).
 //
-// Replaces q8_decode_attention (laguna_mlx/q8_attn.py:102-130: the Metal kernel at :17-99 and
-// the block merge at :126-130) and, for verify blocks, the reference's unfused path
-// (dequantize, cache.py:99-100, then SDPA with the bottom-right causal mask, laguna.py:107,
-// 183-186).
-//
-// Design (CDNA4, gfx950):
-//  * Grid (split, kv head): each workgroup owns a contiguous key range of one sequence and one
-//    KV head and serves every query row of that KV head (G heads x L positions), so each K/V
-//    byte is read from HBM once. The four waves of a workgroup split its range and run fully
-//    independently (no workgroup barrier in the key loop); their partials meet once at the end.
-//  * Per wave, keys stream in tiles of 32 rows with a one-tile prefetch. K and V codes and the
-//    four scale/bias word arrays go straight from global memory to LDS (global_load_lds),
-//    double-buffered, so nothing in flight holds a VGPR and the only wait is one fixed vmcnt.
-//  * Q.K^T: v_mfma_f32_16x16x32_f16. A = 16 key rows x 32 dims of (1024 + code) fp16 pairs (one
-//    v_perm_b32 per pair), B = 32 dims x 16 query rows of q in fp16, one accumulator per quant
-//    group so the affine terms fold out: q.(s c + b) = s (q.(1024 + c)) + (b - 1024 s) sum(q).
-//  * Softmax in the MFMA result layout: a lane holds 8 keys of one query row; the column max is
-//    two cross-lane exchanges; p = exp2(s - m) with scale*log2(e) folded into the scores.
-//  * P.V: v_mfma_f32_16x16x32_f16 with A = V^T (16 dims x 32 keys) read from the LDS tile with
-//    ds_read_b64_tr_b8 (one 8-byte transposed read per operand) and B = P * scale_v in fp16.
-//    The keys of B's k-slots are ordered exactly as the lane already holds them after Q.K^T,
-//    so P never leaves registers. Bias and 1024-offset terms are per-row sums, not per element.
-//  * Partials (m, l, acc[128]) per (split, query row) go to the workspace. The packed kernel
-//    merges them itself (the last workgroup of each sequence and KV head to finish, counted with
-//    one atomic per workgroup); after the general kernel decode_merge_kernel does the merge.
+// Replaces q8_decode_attention (laguna_mlx/q8_attn.py:102-130: the Metal kernel at :17-99 and the
+// block merge at :126-130) and, for verify blocks, the reference's unfused path (dequantize,
+// cache.py:99-100, then SDPA with the bottom-right causal mask, laguna.py:107, 183-186).
 #include "attn_dev.h"
 
 namespace lq {
@@ -33,348 +12,8 @@ namespace {
 
 using namespace attn;
 
-constexpr int WT = 32;       // key rows per wave tile
 constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
-
-// Per wave, per buffer: K and V codes (32 rows x 128 B each; the 16-byte chunk c of row r sits at
-// chunk position c ^ (r & 7) to spread the column reads over the LDS banks) and the scale/bias
-// word arrays ks, kb, vs, vb (32 each).
-struct WaveBuf {
-  uint8_t k[WT * D];
-  uint8_t v[WT * D];
-  uint32_t ks[WT];
-  uint32_t kb[WT];
-  uint32_t vs[WT];
-  uint32_t vb[WT];
-};
-
-template <int NT>
-struct QSmem {
-  union {
-    WaveBuf buf[NWAVE][2];
-    struct {
-      float acc[NWAVE][16 * NT][D];  // wave partials, final merge
-    } fin;
-  };
-  float st[NWAVE][16 * NT][6];  // m, l, wsum0, wsum1, bsum0, bsum1
-};
-
-__device__ __forceinline__ half8_t codes8_as_h8(uint32_t w0, uint32_t w1) {
-  half8_t r;
-  const half2_t a = codes_as_h2(w0, SEL_B01), b = codes_as_h2(w0, SEL_B23);
-  const half2_t c = codes_as_h2(w1, SEL_B01), d = codes_as_h2(w1, SEL_B23);
-  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-  return r;
-}
-
-template <int NT, bool CAUSAL>
-__global__ __launch_bounds__(NTHR) void q8_attn_mfma_kernel(
-    AttnArgs args, DecodePlan plan) {
-  __shared__ QSmem<NT> sm;
-  const uint16_t* __restrict__ q = args.q;
-  const uint8_t* __restrict__ kc = args.kc;
-  const uint16_t* __restrict__ ks = args.ks;
-  const uint16_t* __restrict__ kb = args.kb;
-  const uint8_t* __restrict__ vc = args.vc;
-  const uint16_t* __restrict__ vs = args.vs;
-  const uint16_t* __restrict__ vb = args.vb;
-  float* __restrict__ part_acc = args.part_acc;
-  float2* __restrict__ part_ml = args.part_ml;
-  const int Hkv = args.Hkv, G = args.G, L = args.L;
-  const int64_t cap = args.cap;
-  const float qk_scale_log2 = args.qk_scale_log2;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = tid >> 6;
-  const int x = blockIdx.x;
-  const int hk = blockIdx.y;
-  int b;
-  find_seq(plan, x, b);
-  const int n = plan.len[b];
-  const int c_begin = (x - plan.split_begin[b]) * plan.chunk;
-  const int c_end = min(c_begin + plan.chunk, n);
-  const int sub = (c_end - c_begin + NWAVE - 1) / NWAVE;
-  const int w_begin = min(c_begin + wv * sub, c_end);
-  const int w_end = min(w_begin + sub, c_end);
-  const int ntiles = (w_end - w_begin + WT - 1) / WT;
-  const int R = G * L;            // query rows of this KV head
-  const int Hq = Hkv * G;
-  const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
-
-  const int lc = lane & 15;       // MFMA column (query row within an N tile)
-  const int lq4 = lane >> 4;      // lane group 0..3
-
-  // ---- B operands of Q.K^T: per N tile, group g, half e: 8 dims per lane (fp16)
-  // k-slot j of lane group lq4 in step (g, e) is dim 64 g + 16 lq4 + 8 e + j
-  half8_t qb[NT][2][2];
-  float qsum[NT][2];  // sum over the group's 64 dims of the fp16 q (scaled by qk_scale_log2)
-  int qpos[NT];       // query position i of this lane's column (causal bound)
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int qi = nt * 16 + lc;
-    const bool valid = qi < R;
-    const int gh = valid ? qi / L : 0;
-    const int i = valid ? qi - gh * L : 0;
-    qpos[nt] = i;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + i) * D;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float s = 0.0f;
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4);
-      const uint4 v = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4 + 8);
-      const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t wd = w[4 * e + j];
-          const _Float16 lo = valid ? (_Float16)bf16_to_f32((uint16_t)(wd & 0xffffu)) : (_Float16)0.0f;
-          const _Float16 hi = valid ? (_Float16)bf16_to_f32((uint16_t)(wd >> 16)) : (_Float16)0.0f;
-          qb[nt][g][e][2 * j] = lo;
-          qb[nt][g][e][2 * j + 1] = hi;
-          s += (float)lo + (float)hi;
-        }
-      s += shfl_xor_f(s, 16);
-      s += shfl_xor_f(s, 32);
-      qsum[nt][g] = s * qk_scale_log2;
-    }
-  }
-
-  f4_t oacc[NT][8];  // out^T[16 dt + 4 lq4 + r][column]
-  float m_run[NT], lsum[NT], wsum[NT][2], bsum[NT][2];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    m_run[nt] = -INFINITY;
-    lsum[nt] = 0.0f;
-    wsum[nt][0] = wsum[nt][1] = bsum[nt][0] = bsum[nt][1] = 0.0f;
-  }
-
-  const uint8_t* kbase = kc + row0 * D;
-  const uint8_t* vbase = vc + row0 * D;
-  const uint32_t* ksw = reinterpret_cast<const uint32_t*>(ks + row0 * 2);
-  const uint32_t* kbw = reinterpret_cast<const uint32_t*>(kb + row0 * 2);
-  const uint32_t* vsw = reinterpret_cast<const uint32_t*>(vs + row0 * 2);
-  const uint32_t* vbw = reinterpret_cast<const uint32_t*>(vb + row0 * 2);
-  const int causal_base = n - L;  // query i sees keys t <= causal_base + i
-
-  // Issue tile `jt`'s loads straight into LDS buffer jt & 1 (10 loads per lane): K and V codes
-  // with the chunk swizzle applied on the global side, and the four scale/bias word arrays.
-  auto issue = [&](int jt) {
-    const int t0 = w_begin + jt * WT;
-    const int last = max(w_end - 1, 0);
-    WaveBuf& wb = sm.buf[wv][jt & 1];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = (lane >> 3) + 8 * u;
-      const int64_t t = min(t0 + row, last);
-      const int chunk = (lane & 7) ^ (row & 7);
-      g2l_b128(kbase + t * D + 16 * chunk, wb.k + 1024 * u);
-      g2l_b128(vbase + t * D + 16 * chunk, wb.v + 1024 * u);
-    }
-    const int64_t ts = min(t0 + (lane & 31), last);
-    g2l_b32(lane < 32 ? (const void*)(ksw + ts) : (const void*)(kbw + ts), wb.ks);
-    g2l_b32(lane < 32 ? (const void*)(vsw + ts) : (const void*)(vbw + ts), wb.vs);
-  };
-
-  // Process tile `jt` (its loads complete): scores, softmax, P.V.
-  auto process = [&](int jt) {
-    const int t0 = w_begin + jt * WT;
-    const WaveBuf& wb = sm.buf[wv][jt & 1];
-    // Q.K^T per (row tile mt, N tile nt, group g)
-    f4_t sacc[2][NT][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int r = 16 * mt + lc;  // A row = key; 16 bytes = dims 64 g + 16 lq4 + (0..15)
-        const uint4 c =
-            *reinterpret_cast<const uint4*>(wb.k + r * D + 16 * ((lq4 + 4 * g) ^ (r & 7)));
-        const half8_t a0 = codes8_as_h8(c.x, c.y);
-        const half8_t a1 = codes8_as_h8(c.z, c.w);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          f4_t z = {0.f, 0.f, 0.f, 0.f};
-          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qb[nt][g][0], z, 0, 0, 0);
-          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qb[nt][g][1], z, 0, 0, 0);
-          sacc[mt][nt][g] = z;
-        }
-      }
-    half8_t wbo[NT][2];  // P.V B operands per N tile and quant group
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float sc[2][4];
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        // scale/bias words of this lane's keys 16 mt + 4 lq4 + r
-        const uint4 ksr = *reinterpret_cast<const uint4*>(wb.ks + 16 * mt + 4 * lq4);
-        const uint4 kbr = *reinterpret_cast<const uint4*>(wb.kb + 16 * mt + 4 * lq4);
-        const uint32_t kw[4] = {ksr.x, ksr.y, ksr.z, ksr.w};
-        const uint32_t bw[4] = {kbr.x, kbr.y, kbr.z, kbr.w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = t0 + 16 * mt + 4 * lq4 + r;
-          const float s0 = bf16_to_f32((uint16_t)(kw[r] & 0xffffu));
-          const float s1 = bf16_to_f32((uint16_t)(kw[r] >> 16));
-          const float b0 = bf16_to_f32((uint16_t)(bw[r] & 0xffffu));
-          const float b1 = bf16_to_f32((uint16_t)(bw[r] >> 16));
-          float v = (s0 * qk_scale_log2) * sacc[mt][nt][0][r] + (b0 - 1024.0f * s0) * qsum[nt][0];
-          v += (s1 * qk_scale_log2) * sacc[mt][nt][1][r] + (b1 - 1024.0f * s1) * qsum[nt][1];
-          bool ok = t < w_end;
-          if (CAUSAL) ok = ok && t <= causal_base + qpos[nt];
-          v = ok ? v : -INFINITY;
-          sc[mt][r] = v;
-          tmax = fmaxf(tmax, v);
-        }
-      }
-      tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-      // Lazy rescaling: the reference max m_run only moves when a tile's max exceeds it by more
-      // than RESCALE_LOG2 (so p <= 2^RESCALE_LOG2); the accumulators are rescaled only then.
-      const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
-      float alpha = 1.0f;
-      if (__builtin_amdgcn_ballot_w64(bump)) {
-        const float mn = bump ? tmax : m_run[nt];
-        alpha = m_run[nt] == -INFINITY ? 0.0f : exp2f(m_run[nt] - mn);
-        m_run[nt] = mn;
-        lsum[nt] *= alpha;
-        wsum[nt][0] *= alpha;
-        wsum[nt][1] *= alpha;
-        bsum[nt][0] *= alpha;
-        bsum[nt][1] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
-      }
-      const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];  // no valid key yet
-      // P and the P.V B operands (k-slot j: key 4 lq4 + j for j < 4, 16 + 4 lq4 + j - 4 else)
-      float ls = 0.f, ws0 = 0.f, ws1 = 0.f, bs0 = 0.f, bs1 = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const uint4 vsr = *reinterpret_cast<const uint4*>(wb.vs + 16 * mt + 4 * lq4);
-        const uint4 vbr = *reinterpret_cast<const uint4*>(wb.vb + 16 * mt + 4 * lq4);
-        const uint32_t sw[4] = {vsr.x, vsr.y, vsr.z, vsr.w};
-        const uint32_t bw[4] = {vbr.x, vbr.y, vbr.z, vbr.w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = exp2f(sc[mt][r] - mref);
-          const _Float16 w0 = (_Float16)(p * bf16_to_f32((uint16_t)(sw[r] & 0xffffu)));
-          const _Float16 w1 = (_Float16)(p * bf16_to_f32((uint16_t)(sw[r] >> 16)));
-          wbo[nt][0][4 * mt + r] = w0;
-          wbo[nt][1][4 * mt + r] = w1;
-          ls += p;
-          ws0 += (float)w0;
-          ws1 += (float)w1;
-          bs0 += p * bf16_to_f32((uint16_t)(bw[r] & 0xffffu));
-          bs1 += p * bf16_to_f32((uint16_t)(bw[r] >> 16));
-        }
-      }
-      lsum[nt] += ls;
-      wsum[nt][0] += ws0;
-      wsum[nt][1] += ws1;
-      bsum[nt][0] += bs0;
-      bsum[nt][1] += bs1;
-    }
-    // P.V: A = V^T tile (16 dims x 32 keys) via one transposed LDS read per dim tile. Source
-    // lane s of each 16-lane group addresses key T[s/2] at column offset 8 (s % 2), so result
-    // lane i receives keys T[0..7] of dim i.
-    const int kslot = lc >> 1;
-    const int key = kslot < 4 ? 4 * lq4 + kslot : 16 + 4 * lq4 + (kslot - 4);
-    const uint8_t* vrow = wb.v + key * D + 8 * (lc & 1);
-    const int vsw7 = key & 7;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const v2i_t raw =
-          __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (dt ^ vsw7)));
-      const half8_t a = codes8_as_h8((uint32_t)raw.x, (uint32_t)raw.y);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, wbo[nt][dt >> 2], oacc[nt][dt],
-                                                               0, 0, 0);
-    }
-  };
-
-  // Tile jt + 1's loads are always issued before tile jt is processed (past the last tile they
-  // clamp to one cached row and are never used), so the wait is a fixed count: 10 loads.
-  issue(0);
-  for (int jt = 0; jt < ntiles; ++jt) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
-    issue(jt + 1);
-    asm volatile("s_waitcnt vmcnt(10)" ::: "memory");   // tile jt has landed in LDS
-    process(jt);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // ---- per-wave totals over the 4 lane groups that share a column
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    float v[5] = {lsum[nt], wsum[nt][0], wsum[nt][1], bsum[nt][0], bsum[nt][1]};
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-      v[k] += shfl_xor_f(v[k], 16);
-      v[k] += shfl_xor_f(v[k], 32);
-    }
-    lsum[nt] = v[0];
-    wsum[nt][0] = v[1];
-    wsum[nt][1] = v[2];
-    bsum[nt][0] = v[3];
-    bsum[nt][1] = v[4];
-  }
-  __syncthreads();  // every wave is done with its LDS tiles before they are reused below
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int col = nt * 16 + lc;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sm.fin.acc[wv][col][16 * dt + 4 * lq4 + r] = oacc[nt][dt][r];
-    if (lq4 == 0) {
-      float* st = sm.st[wv][col];
-      st[0] = m_run[nt];
-      st[1] = lsum[nt];
-      st[2] = wsum[nt][0];
-      st[3] = wsum[nt][1];
-      st[4] = bsum[nt][0];
-      st[5] = bsum[nt][1];
-    }
-  }
-  __syncthreads();
-
-  // ---- merge the four waves (log-sum-exp) into the workgroup's partial
-  for (int o = tid; o < R * D; o += NTHR) {
-    const int col = o / D;
-    const int d = o - col * D;
-    const int g = d >> 6;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    float a = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-      const float* st = sm.st[w][col];
-      const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
-      a += e * ((sm.fin.acc[w][col][d] - 1024.0f * st[2 + g]) + st[4 + g]);
-    }
-    part_acc[((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d] = a;
-  }
-  if (tid < R) {
-    const int col = tid;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    float l = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-      const float* st = sm.st[w][col];
-      l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
-    }
-    part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
-  }
-}
 
 // ----------------------------------------------------------------------------------------------
 // Packed kernel for at most 4 query rows per KV head (decode with G <= 4, small verify blocks).
@@ -808,24 +447,8 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 
 }  // namespace
 
-QAttnFn q8_attn_fn(int nt, bool causal) {
-  if (nt == 0) return causal ? q8_attn_packed_kernel<true> : q8_attn_packed_kernel<false>;
-  if (causal) {
-    switch (nt) {
-      case 1: return q8_attn_mfma_kernel<1, true>;
-      case 2: return q8_attn_mfma_kernel<2, true>;
-      case 3: return q8_attn_mfma_kernel<3, true>;
-      case 4: return q8_attn_mfma_kernel<4, true>;
-    }
-  } else {
-    switch (nt) {
-      case 1: return q8_attn_mfma_kernel<1, false>;
-      case 2: return q8_attn_mfma_kernel<2, false>;
-      case 3: return q8_attn_mfma_kernel<3, false>;
-      case 4: return q8_attn_mfma_kernel<4, false>;
-    }
-  }
-  return nullptr;
+QAttnFn q8_attn_fn(bool causal) {
+  return causal ? q8_attn_packed_kernel<true> : q8_attn_packed_kernel<false>;
 }
 
 }  // namespace lq
