@@ -287,7 +287,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
       const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
       if (__builtin_amdgcn_ballot_w64(bump)) {
         const float mn = bump ? tmax : m_run[nt];
-        const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2f(m_run[nt] - mn);
+        const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
         m_run[nt] = mn;
         lsum[nt] *= alpha;
         bsum[nt][0] *= alpha;
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
 #pragma unroll
     for (int w = 0; w < DW; ++w) {
       const float* st = sm.st[w][col];
-      const float e = st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M);
+      const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
       a += e * fmaf(sm.acc[w][col][d], 16777216.0f, st[2 + g]);
     }
     args.part_acc[((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d] = a;
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
 #pragma unroll
     for (int w = 0; w < DW; ++w) {
       const float* st = sm.st[w][col];
-      l += st[0] == -INFINITY ? 0.0f : exp2f(st[0] - M) * st[1];
+      l += st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M) * st[1];
     }
     args.part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
   }

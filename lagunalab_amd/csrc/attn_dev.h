@@ -21,6 +21,11 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr float RESCALE_LOG2 = 8.0f;  // lazy softmax rescale threshold (log2 units)
 
+// 2^x for x <= 0 (softmax weights against a running or merged maximum): the hardware exp2
+// without the library's denormal-range fix-up; results below 2^-126 are negligible next to the
+// maximum's weight 1.
+__device__ __forceinline__ float exp2_nonpos(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // 8 codes (two words) as fp16 subnormals c * 2^-24 for an MFMA operand.
 __device__ __forceinline__ half8_t codes8_sub(uint32_t w0, uint32_t w1) {
   typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
@@ -165,13 +170,14 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
         if (base + NPAR * k < ns) cm = fmaxf(cm, mv[k]);
       const float Mn = fmaxf(M, cm);
       if (Mn != -INFINITY) {
-        const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+        const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mn);
         den *= sc;
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[j] *= sc;
 #pragma unroll
         for (int k = 0; k < MCH; ++k) {
-          const float w = (base + NPAR * k < ns && mv[k] != -INFINITY) ? exp2f(mv[k] - Mn) : 0.0f;
+          const bool use = base + NPAR * k < ns && mv[k] != -INFINITY;
+          const float w = use ? exp2_nonpos(mv[k] - Mn) : 0.0f;
           den += w * lv[k];
 #pragma unroll
           for (int j = 0; j < 4; ++j) a[j] += w * av[k][j];
@@ -198,8 +204,8 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
   }
   if (par == 0 && row < R) {
     const float Mx = fmaxf(M, M1);
-    const float e0 = M == -INFINITY ? 0.0f : exp2f(M - Mx);
-    const float e1 = M1 == -INFINITY ? 0.0f : exp2f(M1 - Mx);
+    const float e0 = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mx);
+    const float e1 = M1 == -INFINITY ? 0.0f : exp2_nonpos(M1 - Mx);
     const float inv = 1.0f / (e0 * den + e1 * den1);
     const float r0v = (e0 * a[0] + e1 * a1.x) * inv, r1v = (e0 * a[1] + e1 * a1.y) * inv;
     const float r2v = (e0 * a[2] + e1 * a1.z) * inv, r3v = (e0 * a[3] + e1 * a1.w) * inv;
@@ -297,7 +303,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float mw = WaveVec<NW>::get(m, w);
-      const float e = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+      const float e = mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M);
       a += e * fmaf(WaveVec<NW>::get(ac, w), out_scale, WaveVec<NW>::get(bs, w));
     }
     st_agent(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
@@ -313,7 +319,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float mw = WaveVec<NW>::get(m, w);
-      lt += mw == -INFINITY ? 0.0f : exp2f(mw - M) * WaveVec<NW>::get(l, w);
+      lt += mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M) * WaveVec<NW>::get(l, w);
     }
     float* pml =
         reinterpret_cast<float*>(args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col);

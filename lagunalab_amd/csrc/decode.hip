@@ -49,7 +49,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
     __syncthreads();
     for (int s = c0 + d; s < c1; s += D) {
       const float2 ml = part_ml[(int64_t)s * Hq + hq];
-      const float w = exp2f(ml.x - M);
+      const float w = __builtin_amdgcn_exp2f(ml.x - M);  // <= 0: the hardware exp2 suffices
       wsh[s - c0] = w;
       den += w * ml.y;
     }

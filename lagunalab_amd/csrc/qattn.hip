@@ -263,7 +263,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     const bool bump = tmax > m_run + RESCALE_LOG2;
     if (__builtin_amdgcn_ballot_w64(bump)) {
       const float mn = bump ? tmax : m_run;
-      const float alpha = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
+      const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
       m_run = mn;
       lsum *= alpha;
       bsum0 *= alpha;
