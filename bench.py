@@ -347,15 +347,23 @@ def run_workload(args):
         vn = torch.randn((1, HKV, L, D), device=dev, generator=g).to(torch.bfloat16)
         out = torch.empty((1, HQ, L, D), dtype=torch.bfloat16, device=dev)
 
-        def call(j):  # append the 5 block rows at 65,536 (the same rows every call), then verify
+        def call(j):  # one fused verify step: append the 5 block rows at 65,536, then verify
             (kc, ks, kb), (vc, vs, vb) = layers[j % nl]
-            st = lib.lq_quantize_append_kv(kn.data_ptr(), vn.data_ptr(), 1, HKV, L, D, kc.data_ptr(),
-                                           ks.data_ptr(), kb.data_ptr(), vc.data_ptr(), vs.data_ptr(),
-                                           vb.data_ptr(), cap, nc, 8, GS, sp)
-            st |= lib.lq_q8_verify_attn(qv.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
-                                        vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, HQ, HKV, L, D,
-                                        cap, nc + L, scale, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                        sp)
+            if args.separate_append:
+                st = lib.lq_quantize_append_kv(kn.data_ptr(), vn.data_ptr(), 1, HKV, L, D,
+                                               kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                               vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), cap, nc,
+                                               8, GS, sp)
+                st |= lib.lq_q8_verify_attn(qv.data_ptr(), kc.data_ptr(), ks.data_ptr(),
+                                            kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(),
+                                            1, HQ, HKV, L, D, cap, nc + L, scale, out.data_ptr(),
+                                            ws.data_ptr(), ws.numel(), sp)
+            else:
+                st = lib.lq_q8_verify_append_attn(qv.data_ptr(), kn.data_ptr(), vn.data_ptr(),
+                                                  kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                                  vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, HQ,
+                                                  HKV, L, D, cap, nc, scale, out.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), sp)
             if st:
                 _lib.check(st, "verify step")
         for j in range(args.warmup):
@@ -370,7 +378,9 @@ def run_workload(args):
                  "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                  "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
                               "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
-                              "kernel": "lq_quantize_append_kv + lq_q8_verify_attn (causal, L=5)",
+                              "kernel": ("lq_quantize_append_kv + lq_q8_verify_attn"
+                                         if args.separate_append else
+                                         "lq_q8_verify_append_attn") + " (causal, L=5)",
                               "bytes_per_call": nbytes}}
         if do_cpu:
             from oracle import attention as A

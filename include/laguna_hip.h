@@ -147,6 +147,21 @@ int lq_q8_verify_attn(const uint16_t* q, const uint8_t* kc, const uint16_t* ks,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * One fused verify step on the 8-bit cache: appends the block's L new key and value rows of
+ * every sequence (bf16 k_new, v_new [B, Hkv, L, D], quantized exactly as lq_quantize_append_kv)
+ * at rows n .. n+L-1 and runs lq_q8_verify_attn over the n + L rows, as
+ * DequantKVCache.update_and_fetch followed by the verify forward's attention
+ * (laguna_mlx/cache.py:89-100; laguna_mlx/dflash.py:195 -> laguna.py:107) -- the append inside
+ * the attention kernel when G * L > 4. n counts the rows BEFORE the append; n + L <= cap.
+ * Workspace: lq_verify_workspace_bytes for n + L rows.
+ */
+int lq_q8_verify_append_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                             uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc, uint16_t* vs,
+                             uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                             int64_t D, int64_t cap, int64_t n, float scale, uint16_t* out,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Prompt-lookup draft search. Replaces NgramIndex.propose (laguna_mlx/dflash.py:164-167) for a
  * history held on the device: finds the most recent start s <= T-g-1 with
  * hist[s:s+g] == hist[T-g:T] and returns up to n following ids (never past T).

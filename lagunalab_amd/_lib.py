@@ -37,6 +37,8 @@ SIGNATURES = {
     "lq_verify_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64]),
     "lq_q8_verify_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64,
                                 f32, vp, vp, i64, vp]),
+    "lq_q8_verify_append_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
+                                       i64, i64, f32, vp, vp, i64, vp]),
     "lq_ngram_workspace_bytes": (i64, [i64]),
     "lq_ngram_propose": (i32, [vp, i64, i32, i32, vp, vp, i64, vp]),
     "lq_accept_workspace_bytes": (i64, [i64, i64]),

@@ -142,10 +142,11 @@ class DequantKVCache:
     (``laguna_mlx/cache.py:66-144``). No ``bits`` attribute except on single-token
     ``quantized_decode`` steps.
 
-    Fused single-token steps (``fused_decode``): ``update_and_fetch`` reserves the new row and
-    ``attend`` quantizes, stores and attends over it in one kernel launch
-    (``lq_q8_decode_append_attn``). Any other use of the cache before ``attend`` (``state``,
-    ``trim``, the next ``update_and_fetch``, indexing the returned tuples) writes the row first."""
+    Fused steps (``fused_decode``; verify blocks of up to 16 rows with ``fused_verify``):
+    ``update_and_fetch`` reserves the new rows and ``attend`` quantizes, stores and attends over
+    them in the attention launch (``lq_q8_decode_append_attn``, ``lq_q8_verify_append_attn``). Any
+    other use of the cache before ``attend`` (``state``, ``trim``, the next ``update_and_fetch``,
+    indexing the returned tuples) writes the rows first."""
 
     def __init__(self, group_size=64, bits=8, quantized_decode=False, fused_decode=False,
                  fused_verify=None):
@@ -170,16 +171,13 @@ class DequantKVCache:
         L = keys.shape[2]
         # Attention checks `fused_step` and then calls attend(); the K/V returned are unused
         self.fused_step = self.fused_decode and (L == 1 or (self.fused_verify and L <= 16))
-        if self.fused_step and L == 1:
+        if self.fused_step:
             row = self.q.reserve(keys, values)
             self._pending = (keys, values, row)
             self._quantized_step = False
             qk, qv = self.q.views()
             return _PendingRows(qk, self), _PendingRows(qv, self)
         qk, qv = self.q.update_and_fetch(keys, values)
-        if self.fused_step:
-            self._quantized_step = False
-            return qk, qv
         self._quantized_step = self.quantized_decode and L == 1
         if self._quantized_step:
             return qk, qv
@@ -189,21 +187,26 @@ class DequantKVCache:
 
     def attend(self, queries, scale):
         """Attention straight off the packed cache: the fused decode kernel for one query row,
-        the fused causal verify kernel for a block of up to 16 rows."""
-        from .q8_attn import decode_append_attention, q8_decode_attention, q8_verify_attention
+        the fused causal verify kernel for a block of up to 16 rows; the step's pending new rows
+        are appended by the same call."""
+        from .q8_attn import (decode_append_attention, q8_decode_attention,
+                              q8_verify_append_attention, q8_verify_attention)
 
-        if queries.shape[2] == 1:
-            if self._pending is not None:
-                k, v, row = self._pending
-                B, Hq, L, D = queries.shape
-                if L != 1 or D != 128:
-                    raise AssertionError("decode only, head_dim 128")
+        L = queries.shape[2]
+        if self._pending is not None and self._pending[0].shape[2] == L:
+            k, v, row = self._pending
+            if queries.shape[3] != 128:
+                raise AssertionError("head_dim 128")
+            self._pending = None
+            if L == 1:
                 out = decode_append_attention(queries.to(torch.bfloat16), k, v, self.q.keys,
                                               self.q.values, n=row, scale=scale)
-                self._pending = None
                 return out.to(queries.dtype)
-            return q8_decode_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
+            return q8_verify_append_attention(queries, k, v, self.q.keys, self.q.values, row,
+                                              scale)
         self._flush()
+        if L == 1:
+            return q8_decode_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
         return q8_verify_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
 
     @property

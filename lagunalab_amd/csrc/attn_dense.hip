@@ -24,6 +24,14 @@
 //  * Work: the waves of a sequence's workgroups take super-tiles gw, gw + NWS, ... (static,
 //    interleaved); K, V and the word arrays of a super-tile go global -> LDS with 20 DMA copies,
 //    double-buffered per wave, one fixed wait per super-tile.
+//  * Fused append (k_new/v_new set): the L new rows n-L .. n-1 of each sequence (one for decode,
+//    the verify block's rows for verify) are quantized at the start by the other waves of the
+//    workgroup(s) whose wave owns their super-tile (the owner has the sequence's last, extra
+//    super-tile and stays off this work), stored to the cache at once and staged in LDS; the
+//    owner patches the staged rows into its LDS copy of the super-tile after the copies land (the
+//    copies may have read the rows before or while they were stored), once an LDS count says the
+//    staging waves are done. No other wave uses those rows. Same arithmetic as
+//    quantize_append_kernel, so the codes agree.
 //  * Partials (m, l, acc) per (workgroup, query row) go to the workspace; decode_merge_kernel
 //    merges them (at 16+ rows per KV head the partials of 32 workgroups are ~330 KB per head, too
 //    much for one workgroup to merge at the end of the attention kernel).
@@ -51,6 +59,8 @@ struct DenseTerms {  // per key of the current super-tile
   float vs0[DST], vs1[DST], vb0[DST], vb1[DST];
 };
 
+constexpr int MAX_NEW = 16;  // rows of a fused append (verify L <= 16)
+
 template <int NT>
 struct DenseSmem {
   union {
@@ -61,6 +71,12 @@ struct DenseSmem {
     alignas(16) float acc[DW][16 * NT][D];  // wave partials (epilogue)
   };
   alignas(16) float st[DW][16 * NT][4];  // m, l, bias sum 0, bias sum 1
+  struct {                             // fused append: new row n - L + j, quantized
+    uint8_t k[MAX_NEW][D];
+    uint8_t v[MAX_NEW][D];
+    uint32_t w[MAX_NEW][4];            // K scale, K bias, V scale, V bias words
+    int ready;                         // staging waves done
+  } stg;
 };
 
 template <int NT, bool CAUSAL>
@@ -90,42 +106,12 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
   const int lc = lane & 15;
   const int lq4 = lane >> 4;
 
-  // ---- B operands of Q.K^T: per N tile, group g, k-step e: q[row 16 nt + lc] dims
-  // 64 g + 16 lq4 + 8 e + (0..7), fp16; qsum: the group's sum of those fp16 values (all lanes
-  // of the column), times scale * log2(e).
+  // B operands of Q.K^T (filled once the first super-tile is in flight): per N tile, group g,
+  // k-step e: q[row 16 nt + lc] dims 64 g + 16 lq4 + 8 e + (0..7), fp16; qsum: the group's sum of
+  // those fp16 values (all lanes of the column), times scale * log2(e).
   half8_t qb[NT][2][2];
   float qsum[NT][2];
   int qpos[NT];  // position i of the query row in its block (causal bound)
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int qr_i = 16 * nt + lc;
-    const bool valid = qr_i < R;
-    const int gh = valid ? qr_i / L : 0;
-    const int i = valid ? qr_i - gh * L : 0;
-    qpos[nt] = i;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + i) * D;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float s = 0.0f;
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4);
-      const uint4 v = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4 + 8);
-      const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t wd = w[4 * e + j];
-          const _Float16 lo = valid ? (_Float16)bf16_lo(wd) : (_Float16)0.0f;
-          const _Float16 hi = valid ? (_Float16)bf16_hi(wd) : (_Float16)0.0f;
-          qb[nt][g][e][2 * j] = lo;
-          qb[nt][g][e][2 * j + 1] = hi;
-          s += (float)lo + (float)hi;
-        }
-      s += shfl_xor_f(s, 16);
-      s += shfl_xor_f(s, 32);
-      qsum[nt][g] = s * qk_scale_log2;
-    }
-  }
 
   f4_t oacc[NT][8];  // out^T[16 dt + 4 lq4 + r][row 16 nt + lc]
   float m_run[NT], lsum[NT], bsum[NT][2];
@@ -146,6 +132,47 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
   const uint32_t* vbw = reinterpret_cast<const uint32_t*>(args.vb + row0 * 2);
   const int causal_base = n - L;  // query i sees keys t <= causal_base + i
   DenseTerms& tm = sm.loop.terms[wv];
+
+  // ---- fused append: super-tiles ta .. tb (at most two) hold the new rows na .. n-1. Super-tile
+  // t belongs to wave t % NWS of the sequence, i.e. to workgroup (t % NWS) / DW; that workgroup
+  // stages the rows of its super-tile(s).
+  const bool app = args.knew != nullptr;
+  const int na = n - L;
+  const int ta = na / DST, tb = (n - 1) / DST;
+  const int xs = x - plan.split_begin[b];
+  const bool wg_a = app && (ta % NWS) / DW == xs;
+  const bool wg_b = app && tb != ta && (tb % NWS) / DW == xs;
+  const int sr0 = wg_a ? na : tb * DST;  // rows staged by this workgroup: [sr0, sr1)
+  const int sr1 = wg_b ? n : min(n, (ta + 1) * DST);
+  const int wa = wg_a ? ta % NWS - DW * xs : -1;  // owner waves in this workgroup (or -1)
+  const int wb = wg_b ? tb % NWS - DW * xs : -1;
+  const int nstage = DW - (wa >= 0) - (wb >= 0);  // staging waves: the others (>= 2)
+  const int si = wv - (wa >= 0 && wa < wv) - (wb >= 0 && wb < wv);  // this wave's staging rank
+  const bool stager = (wg_a || wg_b) && wv != wa && wv != wb;
+  if (wg_a || wg_b) {  // workgroup-uniform; before any copy is issued: nothing to wait for
+    if (tid == 0) sm.stg.ready = 0;
+    __syncthreads();
+  }
+  // Overwrites the new rows of super-tile `tile` in its LDS copy with the staged ones (same
+  // swizzle as the copies: chunk c of row r at chunk position c ^ (r & 7); lane l moves bytes
+  // 2l, 2l+1 = chunk l / 8).
+  auto patch = [&](int tile, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    DenseBuf& pb = sm.loop.buf[wv][BUF];
+    const int t0 = tile * DST;
+    for (int row = max(t0, na); row < min(t0 + DST, n); ++row) {
+      const int j = row - na, r = row - t0;
+      const int off = r * D + 16 * ((lane >> 3) ^ (r & 7)) + 2 * (lane & 7);
+      const uint16_t kc2 = *reinterpret_cast<const uint16_t*>(&sm.stg.k[j][2 * lane]);
+      const uint16_t vc2 = *reinterpret_cast<const uint16_t*>(&sm.stg.v[j][2 * lane]);
+      *reinterpret_cast<uint16_t*>(pb.k + off) = kc2;
+      *reinterpret_cast<uint16_t*>(pb.v + off) = vc2;
+      if (lane < 4) {
+        uint32_t* dst = lane == 0 ? pb.ks : lane == 1 ? pb.kb : lane == 2 ? pb.vs : pb.vb;
+        dst[r] = sm.stg.w[j][lane];
+      }
+    }
+  };
 
   // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
   // bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the LDS row. A
@@ -308,8 +335,10 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
           const float4 vs1 = *reinterpret_cast<const float4*>(tm.vs1 + k0);
           const float4 vb0 = *reinterpret_cast<const float4*>(tm.vb0 + k0);
           const float4 vb1 = *reinterpret_cast<const float4*>(tm.vb1 + k0);
-          const float vs0v[4] = {vs0.x, vs0.y, vs0.z, vs0.w}, vs1v[4] = {vs1.x, vs1.y, vs1.z, vs1.w};
-          const float vb0v[4] = {vb0.x, vb0.y, vb0.z, vb0.w}, vb1v[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
+          const float vs0v[4] = {vs0.x, vs0.y, vs0.z, vs0.w};
+          const float vs1v[4] = {vs1.x, vs1.y, vs1.z, vs1.w};
+          const float vb0v[4] = {vb0.x, vb0.y, vb0.z, vb0.w};
+          const float vb1v[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float p = __builtin_amdgcn_exp2f(sc[nt][mt][r] - mref);
@@ -341,13 +370,14 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
       const int sw = key & 7;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const v2i_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (dt ^ sw)));
+        const v2i_t raw =
+            __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (dt ^ sw)));
         const half8_t a = codes8_sub((uint32_t)raw.x, (uint32_t)raw.y);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const uint32_t* w = pw[nt][e][dt >> 2];
-          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, words_as_h8(w[0], w[1], w[2], w[3]),
-                                                                oacc[nt][dt], 0, 0, 0);
+          const half8_t bw = words_as_h8(w[0], w[1], w[2], w[3]);
+          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, oacc[nt][dt], 0, 0, 0);
         }
       }
     }
@@ -359,18 +389,109 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
   // always issued before the current one is processed (past the end the copies clamp to the last
   // row and are never read), so the wait is a fixed count: the 20 copies issued after it.
   int cur = min(gw, T);
-  issue(cur, B0);
+  issue(cur, B0);  // the first super-tile streams in while q and the new rows are loaded
+  // staging wave: the new rows sr0 + si + nstage i (at most 8 with L <= 16), loads issued
+  // together with q's
+  uint32_t kraw[8], vraw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = sr0 + si + nstage * i;
+    const bool on = stager && row < sr1;
+    const int64_t src = (((int64_t)b * Hkv + hk) * L + (row - na)) * D + 2 * lane;
+    kraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.knew + src) : 0u;
+    vraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.vnew + src) : 0u;
+  }
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int qr_i = 16 * nt + lc;
+    const bool valid = qr_i < R;
+    const int gh = valid ? qr_i / L : 0;
+    const int i = valid ? qr_i - gh * L : 0;
+    qpos[nt] = i;
+    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + i) * D;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float s = 0.0f;
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4);
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4 + 8);
+      const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t wd = w[4 * e + j];
+          const _Float16 lo = valid ? (_Float16)bf16_lo(wd) : (_Float16)0.0f;
+          const _Float16 hi = valid ? (_Float16)bf16_hi(wd) : (_Float16)0.0f;
+          qb[nt][g][e][2 * j] = lo;
+          qb[nt][g][e][2 * j + 1] = hi;
+          s += (float)lo + (float)hi;
+        }
+      s += shfl_xor_f(s, 16);
+      s += shfl_xor_f(s, 32);
+      qsum[nt][g] = s * qk_scale_log2;
+    }
+  }
+
+  if (stager) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = sr0 + si + nstage * i;
+      if (row < sr1) {  // wave-uniform
+        const int j = row - na;
+        const int64_t crow = row0 + row;
+        const QPair kq = quantize_pair_q8(kraw[i]);
+        const QPair vq = quantize_pair_q8(vraw[i]);
+        *reinterpret_cast<uint16_t*>(&sm.stg.k[j][2 * lane]) = (uint16_t)kq.codes;
+        *reinterpret_cast<uint16_t*>(&sm.stg.v[j][2 * lane]) = (uint16_t)vq.codes;
+        *reinterpret_cast<uint16_t*>(args.kc + crow * D + 2 * lane) = (uint16_t)kq.codes;
+        *reinterpret_cast<uint16_t*>(args.vc + crow * D + 2 * lane) = (uint16_t)vq.codes;
+        const uint16_t hv[4] = {kq.scale, kq.bias, vq.scale, vq.bias};
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const uint32_t word = (uint32_t)__builtin_amdgcn_readlane((int)hv[f], 0) |
+                                ((uint32_t)__builtin_amdgcn_readlane((int)hv[f], 32) << 16);
+          if (lane == f) {
+            sm.stg.w[j][f] = word;
+            uint16_t* dst = f == 0 ? args.ks : f == 1 ? args.kb : f == 2 ? args.vs : args.vb;
+            reinterpret_cast<uint32_t*>(dst)[crow] = word;
+          }
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the staged rows are in LDS
+    if (lane == 0)
+      __hip_atomic_fetch_add(&sm.stg.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  // The owner waits (bounded) for the staging waves before its first patch; they finish within
+  // microseconds of the start, long before the owner reaches its last super-tiles.
+  auto staged = [&]() {
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      const int done =
+          __hip_atomic_load(&sm.stg.ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (done >= nstage) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+  };
   for (;;) {
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
     issue(min(cur + NWS, T), B1);
     asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile cur has landed in LDS
+    if (app && (cur == ta || cur == tb)) {
+      staged();
+      patch(cur, B0);
+    }
     process(cur, B0);
     cur = min(cur + NWS, T);
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     issue(min(cur + NWS, T), B0);
     asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    if (app && (cur == ta || cur == tb)) {
+      staged();
+      patch(cur, B1);
+    }
     process(cur, B1);
     cur = min(cur + NWS, T);
   }

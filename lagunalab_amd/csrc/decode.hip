@@ -231,23 +231,11 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
   a.vc = static_cast<uint8_t*>(vc);
   a.vs = vs;
   a.vb = vb;
-  if (k_new) {
-    if (fused_merge) {  // the packed kernel appends the rows itself
-      a.knew = k_new;
-      a.vnew = v_new;
-    } else {  // separate append launch (K and V together), rows len - 1
-      for (int64_t b = 0; b < B; ++b) {
-        const int64_t row = plan.len[b] - 1;
-        const int64_t off = b * Hkv * D;
-        const AppendTarget ta{k_new + off, a.kc + b * Hkv * cap * D, ks + b * Hkv * cap * 2,
-                              kb + b * Hkv * cap * 2};
-        const AppendTarget tb{v_new + off, a.vc + b * Hkv * cap * D, vs + b * Hkv * cap * 2,
-                              vb + b * Hkv * cap * 2};
-        const int rc = quantize_append(ta, tb, 1, 1, Hkv, 1, D, cap, row, 8, 64, st);
-        if (rc != LQ_OK) return rc;
-      }
-    }
+  if (k_new) {  // the packed and the dense kernels append the new row of every sequence themselves
+    a.knew = k_new;
+    a.vnew = v_new;
   }
+
   a.counters = reinterpret_cast<uint32_t*>(workspace);
   a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + WS_COUNTER_BYTES);
   a.part_ml = reinterpret_cast<float2*>(a.part_acc + S * Hq * D);

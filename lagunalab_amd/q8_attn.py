@@ -146,7 +146,8 @@ def decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     """One fused decode step on the 8-bit cache: quantize-append the new rows ``k_new``/``v_new``
     (bf16 ``[B, Hkv, 1, 128]``) at row ``n`` (``lens[b]``) of the full-capacity ``keys``/``values``
     tuples, then attend over ``n + 1`` (``lens[b] + 1``) rows -- ``update_and_fetch`` followed by
-    ``attend`` (``laguna_mlx/cache.py:89-106``) in one kernel launch when Hq / Hkv <= 4.
+    ``attend`` (``laguna_mlx/cache.py:89-106``), the append inside the attention kernel (one launch
+    when Hq / Hkv <= 4, plus the split-merge launch above that).
     ``n`` and ``lens`` count the rows before the append. Returns ``[B, Hq, 1, 128]`` bf16."""
     lib = _lib.load()
     kind, q, (kc, ks, kb), (vc, vs, vb), Hkv, cap = _decode_operands(q, keys, values)
@@ -161,7 +162,8 @@ def decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
             raise ValueError(f"new rows {tuple(t.shape)} do not match {(B, Hkv, 1, D)}")
     for t in (*keys, *values):
         if not t.is_contiguous():
-            raise ValueError("the fused decode step writes the cache in place: its buffers must be contiguous")
+            raise ValueError("the fused decode step writes the cache in place: its buffers must "
+                             "be contiguous")
     lens_arr = after = None
     if lens is not None:
         lens_list = _lens(lens, B)
@@ -243,4 +245,55 @@ def q8_verify_attention(q, keys, values, n, scale):
                                int(n), float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
                                _lib.stream_ptr(dev))
     _lib.check(st, "lq_q8_verify_attn")
+    return out.to(q.dtype)
+
+
+def q8_verify_append_attention(q, k_new, v_new, keys, values, n, scale):
+    """One fused verify step on the 8-bit cache: quantize-append the block's ``L`` new rows
+    ``k_new``/``v_new`` (bf16 ``[B, Hkv, L, 128]``) at rows ``n .. n+L-1`` of the full-capacity
+    ``keys``/``values`` tuples, then the causal verify attention of :func:`q8_verify_attention`
+    over the ``n + L`` rows -- ``update_and_fetch`` then the verify forward's attention
+    (``laguna_mlx/cache.py:89-100``, ``laguna.py:107``), the append inside the attention kernel
+    when G * L > 4. ``n`` counts the rows before the append. Returns [B, Hq, L, 128] in q's
+    dtype."""
+    lib = _lib.load()
+    B, Hq, L, D = q.shape
+    if D != 128 or not 1 <= L <= 16:
+        raise ValueError("verify needs head_dim 128 and 1 <= L <= 16")
+    kc, ks, kb = keys
+    vc, vs, vb = values
+    dev = _lib.require_device(q, k_new, v_new, kc, ks, kb, vc, vs, vb)
+    qb = _bf16(q.to(torch.bfloat16), "q")
+    kc, vc = _as_bytes(kc), _as_bytes(vc)
+    if kc.shape[-1] != D:
+        raise ValueError("verify runs on the 8-bit cache only")
+    ks, kb, vs, vb = (_bf16(t, "scales/biases") for t in (ks, kb, vs, vb))
+    Hkv, cap = kc.shape[1], kc.shape[2]
+    for t in (kc, vc):
+        if tuple(t.shape) != (B, Hkv, cap, D):
+            raise ValueError(f"cache buffer {tuple(t.shape)} does not match {(B, Hkv, cap, D)}")
+    for t in (ks, kb, vs, vb):
+        if tuple(t.shape) != (B, Hkv, cap, D // 64):
+            raise ValueError(f"scales/biases {tuple(t.shape)} do not match {(B, Hkv, cap, D // 64)}")
+    for t in (*keys, *values):
+        if not t.is_contiguous():
+            raise ValueError("the fused verify step writes the cache in place: its buffers must "
+                             "be contiguous")
+    k_new, v_new = _bf16(k_new, "new keys"), _bf16(v_new, "new values")
+    for t in (k_new, v_new):
+        if tuple(t.shape) != (B, Hkv, L, D):
+            raise ValueError(f"new rows {tuple(t.shape)} do not match {(B, Hkv, L, D)}")
+    if not (0 <= int(n) and int(n) + L <= cap):
+        raise ValueError(f"n={n} + {L} new rows must fit the capacity {cap}")
+    ws_bytes = lib.lq_verify_workspace_bytes(B, Hq, Hkv, L, D, int(n) + L)
+    if ws_bytes < 0:
+        raise ValueError(lib.lq_last_error().decode())
+    ws = _workspace(dev, ws_bytes)
+    out = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=dev)
+    st = lib.lq_q8_verify_append_attn(qb.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+                                      kc.data_ptr(), ks.data_ptr(), kb.data_ptr(), vc.data_ptr(),
+                                      vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, L, D, cap, int(n),
+                                      float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      _lib.stream_ptr(dev))
+    _lib.check(st, "lq_q8_verify_append_attn")
     return out.to(q.dtype)

@@ -592,6 +592,36 @@ def test_verify_matches_causal_oracle(dev, n, L, G):
                       f"unfused verify n={n} L={L} G={G}", at, rt)
 
 
+@pytest.mark.parametrize("n,L,G,B", [(0, 5, 4, 1), (100, 5, 4, 1), (4093, 5, 4, 1), (65536, 5, 4, 1),
+                                     (1000, 16, 4, 1), (300, 3, 6, 2), (500, 2, 2, 1), (777, 3, 1, 2),
+                                     (63, 8, 2, 1)])
+def test_fused_verify_step_equals_append_then_verify(dev, n, L, G, B):
+    """lq_q8_verify_append_attn == lq_quantize_append_kv of the block's rows + lq_q8_verify_attn:
+    the same cache bytes (bit-exact) and the same output, for blocks on the dense kernel (G * L > 4,
+    the append inside the kernel, including blocks that straddle two 64-row super-tiles) and on
+    the packed kernel (G * L <= 4, append launch first)."""
+    from lagunalab_amd.q8_attn import q8_verify_append_attention, q8_verify_attention
+    from lagunalab_amd.quant import quantize_kv_into
+    rng = np.random.default_rng(300 + n + L + G)
+    Hkv = 8
+    cap = (n + L + 255) // 256 * 256
+    kq, vq = make_cache(rng, B, Hkv, max(n, 1), cap, dev)
+    kn = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, L, 128)), dev)
+    vn = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, L, 128)), dev)
+    q = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv * G, L, 128)), dev)
+    kf, vf = tuple(t.clone() for t in kq), tuple(t.clone() for t in vq)
+    got = q8_verify_append_attention(q, kn, vn, kf, vf, n, 0.09)
+    quantize_kv_into(kn, vn, kq, vq, n)
+    want = q8_verify_attention(q, kq, vq, n + L, 0.09)
+    for x, y in zip(kf + vf, kq + vq):
+        assert torch.equal(x, y), f"cache differs n={n} L={L} G={G}"
+    assert torch.equal(got, want), f"fused verify step differs n={n} L={L} G={G}"
+    if n + L <= 8192:
+        assert_attn_close(got, A.fused_attention(q.float().cpu().numpy(), cache_np(kq), cache_np(vq),
+                                                 n + L, 0.09, causal=True),
+                          f"fused verify step n={n} L={L} G={G}")
+
+
 def test_verify_single_row_equals_decode(dev):
     from lagunalab_amd.q8_attn import q8_decode_attention, q8_verify_attention
     rng = np.random.default_rng(11)
