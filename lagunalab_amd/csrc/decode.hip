@@ -20,59 +20,46 @@ constexpr int MIN_CHUNK = 128;
 constexpr int64_t MAX_SPLITS = 32;
 
 // ----------------------------------------------------------------------------------------------
-// merge kernel: one workgroup per (sequence, query head), one thread per dim
+// merge kernel: one workgroup per (sequence, partial row), one thread per dim
 // ----------------------------------------------------------------------------------------------
 
-// rows = partial rows per split (Hq * L); one workgroup per (sequence, row), one thread per dim.
+// rows = partial rows per split (Hq * L). A sequence has at most MAX_SPLITS splits (make_plan),
+// so every thread loads all of them -- (m, l) and its dim's acc -- in one round trip and merges
+// them in registers (log-sum-exp against the largest m).
 __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict__ part_acc,
                                                          const float2* __restrict__ part_ml,
                                                          int Hq, DecodePlan plan,
                                                          uint16_t* __restrict__ out) {
-  constexpr int MAXS = 1024;  // splits merged per pass through LDS
-  __shared__ float wsh[MAXS];
-  __shared__ float red[2];
   const int bq = blockIdx.x;
   const int b = bq / Hq;
   const int hq = bq - b * Hq;
   const int d = threadIdx.x;
-  const int s0 = plan.split_begin[b], s1 = plan.split_begin[b + 1];
-  // global max over the sequence's splits: all threads load (m, l) in parallel
-  float M = -INFINITY;
-  for (int s = s0 + d; s < s1; s += D) M = fmaxf(M, part_ml[(int64_t)s * Hq + hq].x);
-  M = wave_max(M);
-  if ((d & 63) == 0) red[d >> 6] = M;
-  __syncthreads();
-  M = fmaxf(red[0], red[1]);
-  float num = 0.0f, den = 0.0f;
-  for (int c0 = s0; c0 < s1; c0 += MAXS) {
-    const int c1 = min(s1, c0 + MAXS);
-    __syncthreads();
-    for (int s = c0 + d; s < c1; s += D) {
-      const float2 ml = part_ml[(int64_t)s * Hq + hq];
-      const float w = __builtin_amdgcn_exp2f(ml.x - M);  // <= 0: the hardware exp2 suffices
-      wsh[s - c0] = w;
-      den += w * ml.y;
-    }
-    __syncthreads();
-    const float* pa = part_acc + ((int64_t)c0 * Hq + hq) * D + d;
-    const int cnt = c1 - c0;
-    int s = 0;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (; s + 4 <= cnt; s += 4) {
-      a0 += wsh[s] * pa[(int64_t)s * Hq * D];
-      a1 += wsh[s + 1] * pa[(int64_t)(s + 1) * Hq * D];
-      a2 += wsh[s + 2] * pa[(int64_t)(s + 2) * Hq * D];
-      a3 += wsh[s + 3] * pa[(int64_t)(s + 3) * Hq * D];
-    }
-    for (; s < cnt; ++s) a0 += wsh[s] * pa[(int64_t)s * Hq * D];
-    num += (a0 + a1) + (a2 + a3);
+  const int s0 = plan.split_begin[b];
+  const int ns = min(plan.split_begin[b + 1] - s0, (int)MAX_SPLITS);
+  float m[MAX_SPLITS], l[MAX_SPLITS], a[MAX_SPLITS];
+  // The (m, l) index is the same in every lane; hidden from the compiler so that the loads stay
+  // vector loads issued together (as scalar loads it waited for each one in turn).
+  int base = s0;
+  asm volatile("" : "+v"(base));
+#pragma unroll
+  for (int k = 0; k < MAX_SPLITS; ++k) {
+    const int64_t r = (int64_t)(base + min(k, ns - 1)) * Hq + hq;
+    const float2 ml = part_ml[r];  // k >= ns: split ns - 1 again, weighted 0 below
+    m[k] = ml.x;
+    l[k] = ml.y;
+    a[k] = part_acc[r * D + d];
   }
-  // den: each thread summed a strided subset of the splits
-  den = wave_sum(den);
-  __syncthreads();
-  if ((d & 63) == 0) red[d >> 6] = den;
-  __syncthreads();
-  den = red[0] + red[1];
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < MAX_SPLITS; ++k) M = fmaxf(M, m[k]);
+  float num = 0.0f, den = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MAX_SPLITS; ++k) {
+    const bool use = k < ns && m[k] != -INFINITY;
+    const float w = use ? __builtin_amdgcn_exp2f(m[k] - M) : 0.0f;  // argument <= 0
+    num = fmaf(w, a[k], num);
+    den = fmaf(w, l[k], den);
+  }
   out[((int64_t)b * Hq + hq) * D + d] = f32_to_bf16(num / den);
 }
 
