@@ -14,7 +14,8 @@
 namespace lq {
 namespace {
 
-constexpr int NG_CHUNK = 4096;  // candidate starts per workgroup (256 threads x 16)
+constexpr int NG_CHUNK = 512;   // candidate starts per workgroup (256 threads x 2): ~160
+                                // workgroups at T = 82,671, each one load round trip
 constexpr int AC_CHUNK = 4096;  // logits per workgroup (256 threads x 16)
 
 __global__ __launch_bounds__(256) void ngram_scan_kernel(const int32_t* __restrict__ hist,
@@ -28,7 +29,7 @@ __global__ __launch_bounds__(256) void ngram_scan_kernel(const int32_t* __restri
   const int64_t S = T - g;  // candidates s in [0, S)
   const int64_t base = (int64_t)blockIdx.x * NG_CHUNK;
   int32_t mine = -1;
-#pragma unroll 4
+#pragma unroll
   for (int k = 0; k < NG_CHUNK / 256; ++k) {
     const int64_t s = base + (int64_t)k * 256 + tid;
     if (s < S) {
@@ -118,34 +119,37 @@ __global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restri
   }
 }
 
-__global__ __launch_bounds__(64) void accept_finish_kernel(const float2* __restrict__ part,
-                                                           int L, int nchunks,
-                                                           const int32_t* __restrict__ drafts,
-                                                           int m, int32_t* __restrict__ out) {
+// One workgroup: the 32 lanes of a row group reduce that row's chunk partials (all rows'
+// loads in one round trip for L <= 8), then k and the next token.
+__global__ __launch_bounds__(256) void accept_finish_kernel(const float2* __restrict__ part,
+                                                            int L, int nchunks,
+                                                            const int32_t* __restrict__ drafts,
+                                                            int m, int32_t* __restrict__ out) {
   __shared__ int32_t pred[64];
-  const int lane = threadIdx.x;
-  for (int row = 0; row < L; ++row) {
+  const int tid = threadIdx.x;
+  const int sub = tid & 31;  // lane within the row's 32-lane group
+  for (int row = tid >> 5; row < L; row += 8) {
     float bv = -INFINITY;
     int32_t bi = INT32_MAX;
-    for (int c = lane; c < nchunks; c += 64) {
+    for (int c = sub; c < nchunks; c += 32) {
       const float2 p = part[(int64_t)row * nchunks + c];
       argmax_merge(bv, bi, p.x, __float_as_int(p.y));
     }
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int off = 16; off >= 1; off >>= 1) {
       const float v2 = __shfl_xor(bv, off, 64);
       const int32_t i2 = __shfl_xor(bi, off, 64);
       argmax_merge(bv, bi, v2, i2);
     }
-    if (lane == 0) pred[row] = bi;
+    if (sub == 0) pred[row] = bi;
   }
   __syncthreads();
-  if (lane == 0) {
+  if (tid == 0) {
     int k = 0;
     while (k < m && drafts[k] == pred[k]) ++k;
     out[0] = k;
     out[1] = pred[k];
   }
-  for (int row = lane; row < L; row += 64) out[2 + row] = pred[row];
+  for (int row = tid; row < L; row += 256) out[2 + row] = pred[row];
 }
 
 }  // namespace
@@ -205,7 +209,7 @@ extern "C" int lq_greedy_accept(const float* logits, int64_t L, int64_t V, const
   float2* part = (float2*)workspace;
   argmax_chunk_kernel<<<dim3(nchunks, (unsigned)L), dim3(256), 0, st>>>(logits, V, nchunks, part);
   LQ_CHECK_LAUNCH("argmax_chunk_kernel");
-  accept_finish_kernel<<<dim3(1), dim3(64), 0, st>>>(part, (int)L, nchunks, drafts, (int)m, out);
+  accept_finish_kernel<<<dim3(1), dim3(256), 0, st>>>(part, (int)L, nchunks, drafts, (int)m, out);
   LQ_CHECK_LAUNCH("accept_finish_kernel");
   return LQ_OK;
 }
