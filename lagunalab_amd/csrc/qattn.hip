@@ -314,44 +314,62 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const std::integral_constant<int, 1> B1;
   // One tile-counter increment by lane 0 when `dyn` (exec narrowed to lane 0 inside the asm, or
   // to no lane for a static step: the same instruction sequence every step, so that the waits
-  // below keep fixed counts), the old value in lane 0 of the returned VGPR. Inline asm like the
+  // below keep fixed counts), the old value landing later in lane 0 of g. Inline asm like the
   // copies, so that the compiler inserts no wait for it: `landed` reads it in the same statement
-  // as the explicit s_waitcnt that covers it (vector memory operations complete in issue order;
-  // each step issues the grab, then the 20 copies of the next super-tile, then waits until only
-  // those 20 are outstanding).
-  auto grab = [&](bool dyn) {
-    uint32_t old;
+  // as the explicit s_waitcnt that covers it, and g is an in-out operand of both statements so
+  // that it stays in its register in between (vector memory operations complete in issue order;
+  // every step ends with a grab and the 20 copies of a super-tile, and waits at its start until
+  // only those are outstanding).
+  auto grab = [&](uint32_t& g, bool dyn) {
     uint64_t sv;
     const uint32_t mask = __builtin_amdgcn_readfirstlane(dyn ? 1u : 0u);
-    asm volatile("s_mov_b64 %1, exec\n\ts_mov_b32 exec_lo, %5\n\ts_mov_b32 exec_hi, 0\n\t"
-                 "global_atomic_add %0, %2, %3, %4 sc0\n\ts_mov_b64 exec, %1"
-                 : "=&v"(old), "=&s"(sv)
-                 : "v"(ctr_off), "v"(1u), "s"(args.counters), "s"(mask)
+    asm volatile("s_mov_b64 %1, exec\n\ts_mov_b32 exec_lo, %4\n\ts_mov_b32 exec_hi, 0\n\t"
+                 "global_atomic_add %0, %2, %5, %3 sc0\n\ts_mov_b64 exec, %1"
+                 : "+v"(g), "=&s"(sv)
+                 : "v"(ctr_off), "s"(args.counters), "s"(mask), "v"(1u)
                  : "memory");
-    return old;
   };
-  // Waits for the current super-tile's copies and the grab issued after them (before the next
-  // super-tile's copies); returns the index of the wave's super-tile number k2 (that after nxt):
-  // static below NS, else the grabbed value past the static ones, clamped to (nxt, T] so that the
-  // loop always advances and every copy address stays inside the sequence.
-  auto landed = [&](uint32_t g, int k2, int nxt_tile) {
+  // Waits for super-tile k (the copies issued before the last grab) and that grab; returns the
+  // index of the wave's super-tile number k + 2: static below NS, else the grabbed value past the
+  // static ones, clamped to (nxt, T] so that the loop always advances and every copy address
+  // stays inside the sequence.
+  auto landed = [&](uint32_t& g, int k2, int nxt_tile) {
     int v;
-    asm volatile("s_waitcnt vmcnt(20)\n\tv_readfirstlane_b32 %0, %1" : "=s"(v) : "v"(g) : "memory");
+    asm volatile("s_waitcnt vmcnt(20)\n\tv_readfirstlane_b32 %0, %1" : "=s"(v), "+v"(g) :: "memory");
     const int t = k2 < NS ? gw + k2 * NWS : NS * NWS + v;
     return min(max(t, nxt_tile + 1), T);
   };
   int cur = min(gw, T), nxt = min(gw + NWS, T);  // wave-uniform super-tile indices
   int k = 0;                                      // cur is the wave's super-tile number k
-  issue(cur, B0);  // the first super-tile streams in while q is loaded and converted
+  uint32_t g = 0u;                                // the grab in flight
+
+  // Prologue, all copies: q rows, the new K and V rows (fused append) into this wave's terms area
+  // (free until the first super-tile is processed), super-tile 0, the grab of super-tile 2 and
+  // super-tile 1. Only the first three are waited for before the q operands are built, so both
+  // super-tiles stream in meanwhile.
+  {
+    const uint32_t stage = lds_addr(&tm);
+    const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;  // the R rows, contiguous
+    dma_b128<0>(qblk, (uint32_t)min(16 * lane, R * 2 * D - 16), stage);
+    if (app) {
+      const int64_t src = ((int64_t)b * Hkv + hk) * D;
+      dma_b32<1024>(args.knew + src, 4u * (uint32_t)lane, stage);
+      dma_b32<1280>(args.vnew + src, 4u * (uint32_t)lane, stage);
+    }
+  }
+  issue(cur, B0);
+  grab(g, false);  // super-tile number 2 (NS >= 2: static)
+  issue(nxt, B1);
+  asm volatile("s_waitcnt vmcnt(41)" ::: "memory");  // the q and new rows have landed
 
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
   {
     const bool on = qvalid && mt == lq4;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
+    const uint8_t* qr = reinterpret_cast<const uint8_t*>(&tm) + (gh * L + qi) * 2 * D;
     float sg[2] = {0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * st);
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * st);
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -369,9 +387,9 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   uint32_t app_w[4] = {0u, 0u, 0u, 0u};  // ks, kb, vs, vb words of the new row (group 0 low)
   bool patched = false;
   if (app) {
-    const int64_t src = ((int64_t)b * Hkv + hk) * D + 2 * lane;
-    app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(args.knew + src));
-    app_v = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(args.vnew + src));
+    const uint8_t* st8 = reinterpret_cast<const uint8_t*>(&tm);
+    app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1024 + 4 * lane));
+    app_v = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1280 + 4 * lane));
     const uint16_t hv[4] = {app_k.scale, app_k.bias, app_v.scale, app_v.bias};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -394,34 +412,33 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     }
   };
 
-  // Unrolled by two so that each buffer's LDS offsets are constants. The next super-tile is
-  // always issued before the current one is processed (past the end the copies clamp to the last
-  // row and are never read), so the wait is a fixed count: the 20 copies of the next super-tile,
-  // issued after the current one's copies and after the grab of the one after next.
+  // Unrolled by two so that each buffer's LDS offsets are constants. Step k waits for super-tile
+  // k, processes it, then refills its buffer with super-tile k + 2 (past the end the copies clamp
+  // to the last row and are never read) after the grab of super-tile k + 3.
   for (;;) {
     if (cur >= T) break;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
-    uint32_t grabbed = grab(k + 2 >= NS);
-    issue(nxt, B1);
-    int after = landed(grabbed, k + 2, nxt);  // super-tile cur and the grab have landed
+    int after = landed(g, k + 2, nxt);
     if (cur == app_t) {
       patch(B0);
       patched = true;
     }
     process(cur, B0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer refilled next are done
+    grab(g, k + 3 >= NS);
+    issue(after, B0);
     cur = nxt;
     nxt = after;
     ++k;
     if (cur >= T) break;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    grabbed = grab(k + 2 >= NS);
-    issue(nxt, B0);
-    after = landed(grabbed, k + 2, nxt);
+    after = landed(g, k + 2, nxt);
     if (cur == app_t) {
       patch(B1);
       patched = true;
     }
     process(cur, B1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    grab(g, k + 3 >= NS);
+    issue(after, B1);
     cur = nxt;
     nxt = after;
     ++k;
