@@ -11,8 +11,9 @@ so the 256 MB last-level cache cannot hold the working set. Inputs are synthetic
 HBM before the timed region starts.
 
 Prints one JSON line: value = algorithmic HBM bytes per second over the timed steps (GB/s), the
-roofline of the decode attention kernel (HIP events on the launch stream around groups of
-back-to-back calls after the timed steps), and the CPU baseline (the oracle's unfused
+roofline of the kernel each step launches (HIP events on the launch stream around the timed
+steps; with --separate-append, around groups of back-to-back attention calls after them), and the
+CPU baseline (the oracle's unfused
 dequantize-to-bf16 + fp32 SDPA path, timed on the host cores).
 """
 from __future__ import annotations
@@ -43,7 +44,8 @@ def parse():
     p.add_argument("--ctx", type=int, default=82671)
     p.add_argument("--layers", type=int, default=10)
     p.add_argument("--roofline-calls", type=int, default=128,
-                   help="attention calls timed for the roofline, in groups of 8, after the timed steps")
+                   help="plain attention calls timed in groups of 8 after the timed steps "
+                        "(attn_us_per_call; the roofline with --separate-append)")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline sample: calls are repeated until this much time has passed")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -576,9 +578,12 @@ def main():
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
 
-    # ---- roofline of the attention kernel: groups of 8 back-to-back lq_decode_attn calls (one
-    # kernel launch each) over the rotating caches, one event pair per group on the launch stream.
-    # Per-call time = group time / 8, which includes the short gap between consecutive launches.
+    # ---- roofline of the dominant kernel. Fused steps: each timed step is exactly one launch of
+    # lq_q8_decode_append_attn, so its average launch duration is the timed region's time / K
+    # (events on the launch stream; this includes the short gap between consecutive launches).
+    # Separate-append steps: groups of 8 back-to-back lq_decode_attn calls over the rotating
+    # caches, one event pair per group, after the timed steps. Either way the plain attention
+    # call is also timed that way and reported as attn_us_per_call.
     group = 8
     pairs, attn_n = [], []
     for gi in range(max(1, args.roofline_calls // group)):
@@ -587,7 +592,7 @@ def main():
         for k in range(group):
             j = gi * group + k
             li = j % nl
-            _lib.check(attend(j % total_steps, layers[li], offsets[li]), "roofline call")
+            _lib.check(attend(j % total_steps, layers[li], offsets[li]), "attention call")
             attn_n.append(offsets[li])
         e[1].record(stream)
         pairs.append(e)
@@ -601,7 +606,13 @@ def main():
     attn_bytes = [Q8_TOKEN * n + 2 * HQ * D * 2 for n in attn_n]
     attn_avg_ms = sum(attn_ms) / len(attn_ms)
     attn_med_ms = sorted(attn_ms)[len(attn_ms) // 2]
-    achieved = (sum(attn_bytes) / len(attn_bytes)) / (attn_avg_ms * 1e-3) / 1e9
+    if args.separate_append:
+        kernel = "lq_decode_attn (q8_attn_packed_kernel, split merge fused)"
+        k_ms, k_bytes, k_calls = attn_avg_ms, sum(attn_bytes) / len(attn_bytes), len(attn_ms) * group
+    else:
+        kernel = "lq_q8_decode_append_attn (q8_attn_packed_kernel: append + attention + split merge)"
+        k_ms, k_bytes, k_calls = total_ms / args.steps, sum(step_bytes) / len(step_bytes), args.steps
+    achieved = k_bytes / (k_ms * 1e-3) / 1e9
 
     traffic = None
     tf = ROOT / "profiles" / "q8_decode_traffic.json"
@@ -629,9 +640,8 @@ def main():
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "lq_decode_attn (q8_attn_packed_kernel, split merge fused)",
-                     "calls_timed": len(attn_ms) * group,
-                     "bytes_per_call": int(sum(attn_bytes) / len(attn_bytes))},
+                     "kernel": kernel, "us_per_launch": round(k_ms * 1e3, 2),
+                     "launches_timed": k_calls, "bytes_per_call": int(k_bytes)},
         "vs_baseline_ref": "reference fused q8 kernel on an M4 GPU: 12.24 ms/call = 14.69 GB/s",
     }
     if not args.no_cpu_baseline and args.cpu_seconds > 0:
