@@ -5,10 +5,10 @@
 // packed cache once, dequantizes in registers and keeps an online softmax per block of keys
 // (:17-99), and the log-sum-exp merge of the block partials (:126-130). The attention kernels
 // themselves (MFMA, global-to-LDS pipeline) are in qattn.hip; this file owns
-//  * the split plan: grid (split, kv head), each workgroup owns a contiguous range of `chunk`
-//    keys of one sequence and one KV head and serves all G query heads of that KV head, so every
-//    K/V byte is read from HBM exactly once; `chunk` is chosen so that the grid is one wave of
-//    resident workgroups over all CUs (no tail), for uniform and ragged batches alike;
+//  * the split plan: grid (split, kv head); the workgroups of one sequence and KV head share its
+//    keys (8-bit kernels: super-tiles in turn; 4-bit and bf16: contiguous chunks) and serve all G
+//    query heads of that KV head, so every K/V byte is read from HBM exactly once; the grid is
+//    one wave of resident workgroups over all CUs, for uniform and ragged batches alike (make_plan);
 //  * the merge: partials (m, l, acc[128]) per (split, query row) are combined per sequence.
 #include "common.h"
 #include "qattn.h"
@@ -68,25 +68,58 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
 // ----------------------------------------------------------------------------------------------
 
 // Builds the split plan. Returns total splits, or -1 on bad lengths.
+//  * Chunked kernels (4-bit, bf16): split s of sequence b covers keys [s chunk, (s + 1) chunk),
+//    one `chunk` for all sequences, sized so that the splits of all sequences fill about one wave
+//    of resident workgroups.
+//  * Interleaved kernels (8-bit): the waves of all of a sequence's splits take its super-tiles in
+//    turn, so only the split count per sequence matters. Each KV head gets at most
+//    wgs_target / Hkv splits (one wave of resident workgroups: nothing waits for a second wave),
+//    apportioned min-max: every sequence starts with one split and each further split goes to
+//    the sequence with the most keys per split, so that the slowest sequence (the one that ends
+//    the launch) has as few keys per split as the budget allows.
 int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_t cap,
-                  int wgs_target, DecodePlan& plan) {
+                  int wgs_target, bool interleaved, DecodePlan& plan) {
   if (B < 1 || B > LQ_MAX_SEQS) return -1;
-  int64_t total = 0;
+  int64_t total = 0, longest = 0;
   for (int64_t b = 0; b < B; ++b) {
     const int64_t l = lens ? lens[b] : n;
     if (l < 1 || (cap > 0 && l > cap)) return -1;
     plan.len[b] = (int32_t)l;
     total += l;
+    longest = std::max<int64_t>(longest, l);
   }
   const int64_t per_head = std::max<int64_t>(1, wgs_target / Hkv);
+  plan.nseq = (int32_t)B;
+  if (interleaved) {
+    int64_t ns[LQ_MAX_SEQS];
+    for (int64_t b = 0; b < B; ++b) ns[b] = 1;
+    for (int64_t budget = per_head - B; budget > 0; --budget) {
+      int64_t best = -1;  // most keys per split among sequences that may take another split
+      for (int64_t b = 0; b < B; ++b) {
+        const int64_t lim =
+            std::min<int64_t>(MAX_SPLITS, (plan.len[b] + MIN_CHUNK - 1) / MIN_CHUNK);
+        if (ns[b] >= lim) continue;
+        if (best < 0 || (int64_t)plan.len[b] * ns[best] > (int64_t)plan.len[best] * ns[b])
+          best = b;
+      }
+      if (best < 0) break;
+      ++ns[best];
+    }
+    int64_t s = 0, chunk = 0;
+    for (int64_t b = 0; b < B; ++b) {
+      plan.split_begin[b] = (int32_t)s;
+      s += ns[b];
+      chunk = std::max<int64_t>(chunk, (plan.len[b] + ns[b] - 1) / ns[b]);
+    }
+    plan.split_begin[B] = (int32_t)s;
+    plan.chunk = (int32_t)chunk;  // largest keys per split (informational)
+    return s;
+  }
   int64_t chunk = (total + per_head - 1) / per_head;
   chunk = std::max<int64_t>(chunk, MIN_CHUNK);
   // at most MAX_SPLITS splits per sequence: the in-kernel merge reads them in one round trip
-  int64_t longest = 0;
-  for (int64_t b = 0; b < B; ++b) longest = std::max<int64_t>(longest, plan.len[b]);
   chunk = std::max<int64_t>(chunk, (longest + MAX_SPLITS - 1) / MAX_SPLITS);
   chunk = (chunk + 15) / 16 * 16;
-  plan.nseq = (int32_t)B;
   plan.chunk = (int32_t)chunk;
   int64_t s = 0;
   for (int64_t b = 0; b < B; ++b) {
@@ -145,7 +178,8 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
   const int64_t S = make_plan(B, Hkv, n, lens, cap,
-                              attn_occupancy(k.fn, k.threads) * device_cu_count(), plan);
+                              attn_occupancy(k.fn, k.threads) * device_cu_count(),
+                              kind == LQ_KV_Q8, plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
   return S;

@@ -100,3 +100,31 @@ def test_lookup_ops_reject_bad_arguments(lib):
 def test_workspace_queries(lib):
     assert lib.lq_ngram_workspace_bytes(82671) >= 4 * (82671 // 4096)
     assert lib.lq_accept_workspace_bytes(5, 131072) == 5 * 32 * 8
+
+
+def test_decode_split_plan_fills_one_wave(lib):
+    """The 8-bit decode plan gives each KV head at most one wave of resident workgroups (256 CUs,
+    one workgroup each, over 8 KV heads: 32 splits per head), apportioned over the sequences by
+    keys per split. The split count is read back from the workspace size: the counter block plus
+    one (m, l, acc[128]) fp32 partial per split, KV head and query row. Without a GPU the host
+    assumes 256 CUs and one resident workgroup per CU."""
+    import ctypes as C
+
+    import numpy as np
+
+    from lagunalab_amd import _lib
+
+    def splits(lens, Hq=32, Hkv=8):
+        arr = (C.c_int32 * len(lens))(*lens)
+        ws = lib.lq_decode_workspace_bytes(8, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
+        per = Hkv * (Hq // Hkv) * (128 * 4 + 8)
+        assert (ws - _lib.LQ_WS_ZERO_BYTES) % per == 0
+        return (ws - _lib.LQ_WS_ZERO_BYTES) // per
+
+    # config 3's lengths: a shared chunk would need 34 splits (a second, partial wave)
+    c3 = [int(x) for x in np.random.default_rng(1).integers(42771, 82672, size=8)]
+    assert splits(c3) == 32
+    assert splits([82671]) == 32
+    assert splits([1000]) == 8        # at least 128 keys per split
+    assert splits([1, 1, 1]) == 3     # one split per sequence at least
+    assert splits([5000] * 40) == 40  # more sequences than the budget: one split each
