@@ -42,31 +42,34 @@ namespace {
 
 using namespace attn;
 
-constexpr int DST = 64;  // keys per super-tile
-constexpr int DW = 4;    // waves per workgroup
+constexpr int DW = 4;  // waves per workgroup
 
+// ST keys per super-tile: 64 (one workgroup per CU) or 32 (about 80 KB of LDS per workgroup, two
+// workgroups per CU: two waves per SIMD hide each other's MFMA, LDS and exp latency).
+template <int ST>
 struct DenseBuf {
-  uint8_t k[DST * D];
-  uint8_t v[DST * D];
-  uint32_t ks[DST];
-  uint32_t kb[DST];
-  uint32_t vs[DST];
-  uint32_t vb[DST];
+  uint8_t k[ST * D];
+  uint8_t v[ST * D];
+  uint32_t ks[ST];
+  uint32_t kb[ST];
+  uint32_t vs[ST];
+  uint32_t vb[ST];
 };
 
+template <int ST>
 struct DenseTerms {  // per key of the current super-tile
-  float ks0[DST], ks1[DST], ku0[DST], ku1[DST];  // s_g * scale*log2e * 2^24, b_g
-  float vs0[DST], vs1[DST], vb0[DST], vb1[DST];
+  float ks0[ST], ks1[ST], ku0[ST], ku1[ST];  // s_g * scale*log2e * 2^24, b_g
+  float vs0[ST], vs1[ST], vb0[ST], vb1[ST];
 };
 
 constexpr int MAX_NEW = 16;  // rows of a fused append (verify L <= 16)
 
-template <int NT>
+template <int NT, int ST>
 struct DenseSmem {
   union {
     struct {
-      DenseBuf buf[DW][2];
-      DenseTerms terms[DW];
+      DenseBuf<ST> buf[DW][2];
+      DenseTerms<ST> terms[DW];
     } loop;
     alignas(16) float acc[DW][16 * NT][D];  // wave partials (epilogue)
   };
@@ -79,9 +82,25 @@ struct DenseSmem {
   } stg;
 };
 
-template <int NT, bool CAUSAL>
-__global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, DecodePlan plan) {
-  __shared__ DenseSmem<NT> sm;
+// Global -> LDS copy of one dword per lane from a per-lane 64-bit address into lds + 4 lane.
+__device__ __forceinline__ void dma_b32_v(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(lds) : "memory");
+}
+
+template <int NT, bool CAUSAL, int ST>
+__global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kernel(AttnArgs args,
+                                                                                 DecodePlan plan) {
+  static_assert(ST == 32 || ST == 64, "super-tiles of 32 or 64 keys");
+  constexpr int MT = ST / 16;  // M tiles (16 keys) per super-tile
+  constexpr int EK = ST / 32;  // P.V k-steps (32 keys) per super-tile
+  // copies per super-tile: K and V codes 1 KB each (8 rows), then the word arrays (four of
+  // ST dwords; with ST = 32 two copies of 64 lanes, each lane addressing its own array)
+  constexpr int NCOPY = ST / 4 + (ST == 64 ? 4 : 2);
+  using DenseBuf = lq::DenseBuf<ST>;
+  using DenseTerms = lq::DenseTerms<ST>;
+  constexpr int DST = ST;
+  __shared__ DenseSmem<NT, ST> sm;
   const uint16_t* __restrict__ q = args.q;
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
@@ -174,16 +193,20 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     }
   };
 
-  // 20 copies per super-tile: 8 K + 8 V (1 KB each) + 4 word arrays. Copy u of lane l moves 16
-  // bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the LDS row. A
-  // full super-tile uses the scalar row base t0 and per-lane offsets that never change; the last
-  // one clamps rows to the sequence's last row, and so do super-tiles past the end (their copies
-  // land in a buffer that is never read).
+  // NCOPY copies per super-tile: ST / 8 K + ST / 8 V (1 KB each) + the word arrays. Copy u of lane
+  // l moves 16 bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the
+  // LDS row. A full super-tile uses the scalar row base t0 and per-lane offsets that never change;
+  // the last one clamps rows to the sequence's last row, and so do super-tiles past the end (their
+  // copies land in a buffer that is never read). With ST = 32 the word arrays go two per copy:
+  // lanes 0-31 read K scale (V scale) words, lanes 32-63 K bias (V bias) words, into the adjacent
+  // ks/kb (vs/vb) arrays of the buffer.
   const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
   const uint32_t col_off = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
-  uint32_t row_off[8];
+  uint32_t row_off[ST / 8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
+  for (int u = 0; u < ST / 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
+  const uint32_t* wsel0 = lane < 32 ? ksw : kbw;  // ST = 32: this lane's word arrays
+  const uint32_t* wsel1 = lane < 32 ? vsw : vbw;
   auto issue = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * DST;
@@ -194,7 +217,8 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     const uint8_t* kb0 = kbase;
     const uint8_t* vb0 = vbase;
     const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
-    uint32_t ro[8], wo;
+    uint32_t ro[ST / 8], wo;
+    int wrow;  // ST = 32: word row of this lane
     if (t0 + DST <= n) {
       kb0 += (int64_t)t0 * D;
       vb0 += (int64_t)t0 * D;
@@ -203,13 +227,15 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
       w2 += t0;
       w3 += t0;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) ro[u] = row_off[u];
+      for (int u = 0; u < ST / 8; ++u) ro[u] = row_off[u];
       wo = 4u * (uint32_t)lane;
+      wrow = t0 + (lane & 31);
     } else {
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < ST / 8; ++u)
         ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last_row) * D + col_off;
       wo = 4u * (uint32_t)min(t0 + lane, last_row);
+      wrow = min(t0 + (lane & 31), last_row);
     }
     dma_b128<OK + 0>(kb0, ro[0], lb);
     dma_b128<OV + 0>(vb0, ro[0], lb);
@@ -219,18 +245,24 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     dma_b128<OV + 2048>(vb0, ro[2], lb);
     dma_b128<OK + 3072>(kb0, ro[3], lb);
     dma_b128<OV + 3072>(vb0, ro[3], lb);
-    dma_b128<OK + 4096>(kb0, ro[4], lb);
-    dma_b128<OV + 4096>(vb0, ro[4], lb);
-    dma_b128<OK + 5120>(kb0, ro[5], lb);
-    dma_b128<OV + 5120>(vb0, ro[5], lb);
-    dma_b128<OK + 6144>(kb0, ro[6], lb);
-    dma_b128<OV + 6144>(vb0, ro[6], lb);
-    dma_b128<OK + 7168>(kb0, ro[7], lb);
-    dma_b128<OV + 7168>(vb0, ro[7], lb);
-    dma_b32<OKS>(w0, wo, lb);
-    dma_b32<OKB>(w1, wo, lb);
-    dma_b32<OVS>(w2, wo, lb);
-    dma_b32<OVB>(w3, wo, lb);
+    if constexpr (ST == 64) {
+      dma_b128<OK + 4096>(kb0, ro[4 % (ST / 8)], lb);
+      dma_b128<OV + 4096>(vb0, ro[4 % (ST / 8)], lb);
+      dma_b128<OK + 5120>(kb0, ro[5 % (ST / 8)], lb);
+      dma_b128<OV + 5120>(vb0, ro[5 % (ST / 8)], lb);
+      dma_b128<OK + 6144>(kb0, ro[6 % (ST / 8)], lb);
+      dma_b128<OV + 6144>(vb0, ro[6 % (ST / 8)], lb);
+      dma_b128<OK + 7168>(kb0, ro[7 % (ST / 8)], lb);
+      dma_b128<OV + 7168>(vb0, ro[7 % (ST / 8)], lb);
+      dma_b32<OKS>(w0, wo, lb);
+      dma_b32<OKB>(w1, wo, lb);
+      dma_b32<OVS>(w2, wo, lb);
+      dma_b32<OVB>(w3, wo, lb);
+    } else {
+      static_assert(OKB == OKS + 4 * ST && OVB == OVS + 4 * ST, "word arrays adjacent");
+      dma_b32_v(wsel0 + wrow, lb + OKS);
+      dma_b32_v(wsel1 + wrow, lb + OVS);
+    }
   };
 
   const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
@@ -239,7 +271,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * DST;
     const DenseBuf& pb = sm.loop.buf[wv][BUF];
-    {  // per-key terms, one lane per key
+    if (ST == 64 || lane < ST) {  // per-key terms, one lane per key
       const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
       tm.ks0[lane] = bf16_lo(a) * kscale;
       tm.ks1[lane] = bf16_hi(a) * kscale;
@@ -251,9 +283,9 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
       tm.vb1[lane] = bf16_hi(f);
     }
     // Q.K^T: c[mt][nt][g]
-    f4_t c[4][NT][2];
+    f4_t c[MT][NT][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const int r = 16 * mt + lc;
       const uint8_t* kr = pb.k + r * D;
 #pragma unroll
@@ -275,9 +307,9 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool full = t0 + DST <= n && (!CAUSAL || t0 + DST - 1 <= causal_base);
     // scores of this lane's keys 16 mt + 4 lq4 + r, per N tile (per-key terms read per M tile)
-    float sc[NT][4][4];
+    float sc[NT][MT][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const int k0 = 16 * mt + 4 * lq4;
       const float4 s0 = *reinterpret_cast<const float4*>(tm.ks0 + k0);
       const float4 s1 = *reinterpret_cast<const float4*>(tm.ks1 + k0);
@@ -301,12 +333,12 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
           sc[nt][mt][r] = v;
         }
     }
-    uint32_t pw[NT][2][2][4];  // P.V B operands: [nt][k-step e][group][dword]
+    uint32_t pw[NT][EK][2][4];  // P.V B operands: [nt][k-step e][group][dword]
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       float tmax = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[nt][mt][r]);
       tmax = max_xor16(tmax);
@@ -325,7 +357,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
       const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float ls = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < EK; ++e) {
         float w0[8], w1[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -363,7 +395,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     // lane s of each 16-lane group addresses key T[s/2] at column offset 8 (s % 2), so result
     // lane i receives keys T[0..7] of dim i.
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < EK; ++e) {
       const int kslot = lc >> 1;
       const int key = 32 * e + (kslot < 4 ? 4 * lq4 + kslot : 16 + 4 * lq4 + (kslot - 4));
       const uint8_t* vrow = pb.v + key * D + 8 * (lc & 1);
@@ -463,6 +495,13 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     if (lane == 0)
       __hip_atomic_fetch_add(&sm.stg.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+  // Waits until only the NCOPY copies of the super-tile issued last are outstanding.
+  auto wait_tile = [&]() {
+    if constexpr (NCOPY == 20)
+      asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  };
   // The owner waits (bounded) for the staging waves before its first patch; they finish within
   // microseconds of the start, long before the owner reaches its last super-tiles.
   auto staged = [&]() {
@@ -477,7 +516,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
     issue(min(cur + NWS, T), B1);
-    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");   // super-tile cur has landed in LDS
+    wait_tile();  // super-tile cur has landed in LDS
     if (app && (cur == ta || cur == tb)) {
       staged();
       patch(cur, B0);
@@ -487,7 +526,7 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     issue(min(cur + NWS, T), B0);
-    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    wait_tile();
     if (app && (cur == ta || cur == tb)) {
       staged();
       patch(cur, B1);
@@ -556,20 +595,22 @@ __global__ __launch_bounds__(64 * DW) void q8_attn_dense_kernel(AttnArgs args, D
 
 }  // namespace
 
+// Up to 32 query rows per KV head: 32-key super-tiles, two workgroups per CU. More rows: 64-key
+// super-tiles (their wave partials need the LDS of a whole CU).
 QAttnFn q8_dense_attn_fn(int nt, bool causal) {
   if (causal) {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, true>;
-      case 2: return q8_attn_dense_kernel<2, true>;
-      case 3: return q8_attn_dense_kernel<3, true>;
-      case 4: return q8_attn_dense_kernel<4, true>;
+      case 1: return q8_attn_dense_kernel<1, true, 32>;
+      case 2: return q8_attn_dense_kernel<2, true, 32>;
+      case 3: return q8_attn_dense_kernel<3, true, 64>;
+      case 4: return q8_attn_dense_kernel<4, true, 64>;
     }
   } else {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, false>;
-      case 2: return q8_attn_dense_kernel<2, false>;
-      case 3: return q8_attn_dense_kernel<3, false>;
-      case 4: return q8_attn_dense_kernel<4, false>;
+      case 1: return q8_attn_dense_kernel<1, false, 32>;
+      case 2: return q8_attn_dense_kernel<2, false, 32>;
+      case 3: return q8_attn_dense_kernel<3, false, 64>;
+      case 4: return q8_attn_dense_kernel<4, false, 64>;
     }
   }
   return nullptr;

@@ -17,13 +17,14 @@ namespace lq {
 namespace {
 
 constexpr int MIN_CHUNK = 128;
-constexpr int64_t MAX_SPLITS = 32;
+constexpr int64_t MAX_SPLITS = 32;    // kernels that merge their own splits (merge_rows4)
+constexpr int64_t MERGE_SPLITS = 64;  // kernels whose splits decode_merge_kernel merges
 
 // ----------------------------------------------------------------------------------------------
 // merge kernel: one workgroup per (sequence, partial row), one thread per dim
 // ----------------------------------------------------------------------------------------------
 
-// rows = partial rows per split (Hq * L). A sequence has at most MAX_SPLITS splits (make_plan),
+// rows = partial rows per split (Hq * L). A sequence has at most MERGE_SPLITS splits (make_plan),
 // so every thread loads all of them -- (m, l) and its dim's acc -- in one round trip and merges
 // them in registers (log-sum-exp against the largest m).
 __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict__ part_acc,
@@ -35,14 +36,14 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
   const int hq = bq - b * Hq;
   const int d = threadIdx.x;
   const int s0 = plan.split_begin[b];
-  const int ns = min(plan.split_begin[b + 1] - s0, (int)MAX_SPLITS);
-  float m[MAX_SPLITS], l[MAX_SPLITS], a[MAX_SPLITS];
+  const int ns = min(plan.split_begin[b + 1] - s0, (int)MERGE_SPLITS);
+  float m[MERGE_SPLITS], l[MERGE_SPLITS], a[MERGE_SPLITS];
   // The (m, l) index is the same in every lane; hidden from the compiler so that the loads stay
   // vector loads issued together (as scalar loads it waited for each one in turn).
   int base = s0;
   asm volatile("" : "+v"(base));
 #pragma unroll
-  for (int k = 0; k < MAX_SPLITS; ++k) {
+  for (int k = 0; k < MERGE_SPLITS; ++k) {
     const int64_t r = (int64_t)(base + min(k, ns - 1)) * Hq + hq;
     const float2 ml = part_ml[r];  // k >= ns: split ns - 1 again, weighted 0 below
     m[k] = ml.x;
@@ -51,10 +52,10 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < MAX_SPLITS; ++k) M = fmaxf(M, m[k]);
+  for (int k = 0; k < MERGE_SPLITS; ++k) M = fmaxf(M, m[k]);
   float num = 0.0f, den = 0.0f;
 #pragma unroll
-  for (int k = 0; k < MAX_SPLITS; ++k) {
+  for (int k = 0; k < MERGE_SPLITS; ++k) {
     const bool use = k < ns && m[k] != -INFINITY;
     const float w = use ? __builtin_amdgcn_exp2f(m[k] - M) : 0.0f;  // argument <= 0
     num = fmaf(w, a[k], num);
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict
 //    the sequence with the most keys per split, so that the slowest sequence (the one that ends
 //    the launch) has as few keys per split as the budget allows.
 int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_t cap,
-                  int wgs_target, bool interleaved, DecodePlan& plan) {
+                  int wgs_target, bool interleaved, int64_t max_splits, DecodePlan& plan) {
   if (B < 1 || B > LQ_MAX_SEQS) return -1;
   int64_t total = 0, longest = 0;
   for (int64_t b = 0; b < B; ++b) {
@@ -97,7 +98,7 @@ int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_
       int64_t best = -1;  // most keys per split among sequences that may take another split
       for (int64_t b = 0; b < B; ++b) {
         const int64_t lim =
-            std::min<int64_t>(MAX_SPLITS, (plan.len[b] + MIN_CHUNK - 1) / MIN_CHUNK);
+            std::min<int64_t>(max_splits, (plan.len[b] + MIN_CHUNK - 1) / MIN_CHUNK);
         if (ns[b] >= lim) continue;
         if (best < 0 || (int64_t)plan.len[b] * ns[best] > (int64_t)plan.len[best] * ns[b])
           best = b;
@@ -117,8 +118,8 @@ int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_
   }
   int64_t chunk = (total + per_head - 1) / per_head;
   chunk = std::max<int64_t>(chunk, MIN_CHUNK);
-  // at most MAX_SPLITS splits per sequence: the in-kernel merge reads them in one round trip
-  chunk = std::max<int64_t>(chunk, (longest + MAX_SPLITS - 1) / MAX_SPLITS);
+  // at most max_splits splits per sequence: the in-kernel merge reads them in one round trip
+  chunk = std::max<int64_t>(chunk, (longest + max_splits - 1) / max_splits);
   chunk = (chunk + 15) / 16 * 16;
   plan.chunk = (int32_t)chunk;
   int64_t s = 0;
@@ -177,9 +178,12 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   }
   if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
-  const int64_t S = make_plan(B, Hkv, n, lens, cap,
-                              attn_occupancy(k.fn, k.threads) * device_cu_count(),
-                              kind == LQ_KV_Q8, plan);
+  // One workgroup per CU for the dense kernel too: with 32-key super-tiles two would fit, but
+  // measured at 65,541 keys and 20 rows per KV head, 32 splits per head (36.4 us) beat 64 (37.8).
+  const int per_cu = attn_merges_itself(R) || kind != LQ_KV_Q8 ? attn_occupancy(k.fn, k.threads) : 1;
+  const int64_t S = make_plan(B, Hkv, n, lens, cap, per_cu * device_cu_count(),
+                              kind == LQ_KV_Q8, attn_merges_itself(R) ? MAX_SPLITS : MERGE_SPLITS,
+                              plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
   return S;
