@@ -21,47 +21,57 @@ constexpr int64_t MAX_SPLITS = 32;    // kernels that merge their own splits (me
 constexpr int64_t MERGE_SPLITS = 64;  // kernels whose splits decode_merge_kernel merges
 
 // ----------------------------------------------------------------------------------------------
-// merge kernel: one workgroup per (sequence, partial row), one thread per dim
+// merge kernel: four partial rows per workgroup, four dims per thread
 // ----------------------------------------------------------------------------------------------
 
-// rows = partial rows per split (Hq * L). A sequence has at most MERGE_SPLITS splits (make_plan),
-// so every thread loads all of them -- (m, l) and its dim's acc -- in one round trip and merges
-// them in registers (log-sum-exp against the largest m).
-__global__ __launch_bounds__(D) void decode_merge_kernel(const float* __restrict__ part_acc,
-                                                         const float2* __restrict__ part_ml,
-                                                         int Hq, DecodePlan plan,
-                                                         uint16_t* __restrict__ out) {
-  const int bq = blockIdx.x;
-  const int b = bq / Hq;
-  const int hq = bq - b * Hq;
-  const int d = threadIdx.x;
+// rows = partial rows per sequence (Hq * L). A sequence has at most MS <= MERGE_SPLITS splits
+// (make_plan), so every thread loads all of them -- (m, l) and the 16 bytes of acc of its four
+// dims -- in one round trip and merges them in registers (log-sum-exp against the largest m).
+template <int MS>
+__global__ __launch_bounds__(128) void decode_merge_kernel(const float* __restrict__ part_acc,
+                                                           const float2* __restrict__ part_ml,
+                                                           int rows, int total_rows,
+                                                           DecodePlan plan,
+                                                           uint16_t* __restrict__ out) {
+  const int grow = blockIdx.x * 4 + (threadIdx.x >> 5);  // (sequence, row) index
+  if (grow >= total_rows) return;
+  const int b = grow / rows;
+  const int hq = grow - b * rows;
+  const int d0 = 4 * (threadIdx.x & 31);
   const int s0 = plan.split_begin[b];
-  const int ns = min(plan.split_begin[b + 1] - s0, (int)MERGE_SPLITS);
-  float m[MERGE_SPLITS], l[MERGE_SPLITS], a[MERGE_SPLITS];
-  // The (m, l) index is the same in every lane; hidden from the compiler so that the loads stay
+  const int ns = min(plan.split_begin[b + 1] - s0, MS);
+  float m[MS], l[MS];
+  float4 a[MS];
+  // The (m, l) index is the same in 32 lanes; hidden from the compiler so that the loads stay
   // vector loads issued together (as scalar loads it waited for each one in turn).
   int base = s0;
   asm volatile("" : "+v"(base));
 #pragma unroll
-  for (int k = 0; k < MERGE_SPLITS; ++k) {
-    const int64_t r = (int64_t)(base + min(k, ns - 1)) * Hq + hq;
+  for (int k = 0; k < MS; ++k) {
+    const int64_t r = (int64_t)(base + min(k, ns - 1)) * rows + hq;
     const float2 ml = part_ml[r];  // k >= ns: split ns - 1 again, weighted 0 below
     m[k] = ml.x;
     l[k] = ml.y;
-    a[k] = part_acc[r * D + d];
+    a[k] = *reinterpret_cast<const float4*>(part_acc + r * D + d0);
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < MERGE_SPLITS; ++k) M = fmaxf(M, m[k]);
-  float num = 0.0f, den = 0.0f;
+  for (int k = 0; k < MS; ++k) M = fmaxf(M, m[k]);
+  float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f, den = 0.0f;
 #pragma unroll
-  for (int k = 0; k < MERGE_SPLITS; ++k) {
+  for (int k = 0; k < MS; ++k) {
     const bool use = k < ns && m[k] != -INFINITY;
     const float w = use ? __builtin_amdgcn_exp2f(m[k] - M) : 0.0f;  // argument <= 0
-    num = fmaf(w, a[k], num);
+    n0 = fmaf(w, a[k].x, n0);
+    n1 = fmaf(w, a[k].y, n1);
+    n2 = fmaf(w, a[k].z, n2);
+    n3 = fmaf(w, a[k].w, n3);
     den = fmaf(w, l[k], den);
   }
-  out[((int64_t)b * Hq + hq) * D + d] = f32_to_bf16(num / den);
+  const float inv = 1.0f / den;
+  const uint32_t lo = (uint32_t)f32_to_bf16(n0 * inv) | ((uint32_t)f32_to_bf16(n1 * inv) << 16);
+  const uint32_t hi = (uint32_t)f32_to_bf16(n2 * inv) | ((uint32_t)f32_to_bf16(n3 * inv) << 16);
+  *reinterpret_cast<uint2*>(out + (int64_t)grow * D + d0) = make_uint2(lo, hi);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -155,8 +165,16 @@ int attn_occupancy(QAttnFn fn, int threads) {
 
 void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq,
                   const DecodePlan& plan, int64_t B, uint16_t* out, hipStream_t st) {
-  decode_merge_kernel<<<dim3((unsigned)(B * rows_per_seq)), dim3(D), 0, st>>>(
-      part_acc, part_ml, rows_per_seq, plan, out);
+  int most = 1;
+  for (int64_t b = 0; b < B; ++b)
+    most = std::max(most, plan.split_begin[b + 1] - plan.split_begin[b]);
+  const int total = (int)(B * rows_per_seq);
+  const dim3 grid((unsigned)((total + 3) / 4)), block(128);
+  if (most <= 32)
+    decode_merge_kernel<32><<<grid, block, 0, st>>>(part_acc, part_ml, rows_per_seq, total, plan, out);
+  else
+    decode_merge_kernel<MERGE_SPLITS><<<grid, block, 0, st>>>(part_acc, part_ml, rows_per_seq, total,
+                                                              plan, out);
 }
 
 bool attn_merges_itself(int64_t rows_per_kv_head) { return rows_per_kv_head <= 4; }
