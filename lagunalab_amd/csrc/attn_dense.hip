@@ -82,9 +82,10 @@ struct DenseSmem {
   } stg;
 };
 
-// Global -> LDS copy of one dword per lane from a per-lane 64-bit address into lds + 4 lane.
+// Global -> LDS copy of one dword per lane from a per-lane 64-bit address into lds + 4 lane
+// (non-temporal, like the other copies).
 __device__ __forceinline__ void dma_b32_v(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
                :: "v"(g), "s"(lds) : "memory");
 }
 

@@ -51,16 +51,19 @@ __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(
 // blanket vmcnt(0) in front of every LDS read, which would wait for the prefetched tile too.
 // Every wait on these copies is explicit (s_waitcnt vmcnt(N) with the count of copies issued
 // after the ones needed).
+// The copies carry the non-temporal hint (nt): the cache streams through once per call, and
+// marking it streaming keeps it from displacing other lines (measured on the 8-bit decode at
+// 82,671 keys over 10 rotating layer caches: 42.8 -> 40.8 us per launch).
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
 __device__ __forceinline__ void g2l_b32(const void* g, void* lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
                :: "v"(g), "s"(lds_u32(lds_base)) : "memory");
 }
 __device__ __forceinline__ void g2l_b128(const void* g, void* lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
                :: "v"(g), "s"(lds_u32(lds_base)) : "memory");
 }
 // Same copies with a wave-uniform global base (SGPR pair) plus a 32-bit per-lane offset, into
@@ -70,12 +73,12 @@ __device__ __forceinline__ void g2l_b128(const void* g, void* lds_base) {
 // keep a carry live across the statement).
 template <int LOFF>
 __device__ __forceinline__ void dma_b128(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
 }
 template <int LOFF>
 __device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1 nt"
                :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
