@@ -358,7 +358,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     }
   }
   issue(cur, B0);
-  grab(g, false);  // super-tile number 2 (NS >= 2: static)
+  grab(g, 2 >= NS);  // super-tile number 2: dynamic when NS == 2
   issue(nxt, B1);
   asm volatile("s_waitcnt vmcnt(41)" ::: "memory");  // the q and new rows have landed
 

@@ -168,6 +168,28 @@ def test_decode_matches_unfused_oracle(dev, n, G, B):
     assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale), f"unfused n={n} G={G}", at, rt)
 
 
+@pytest.mark.parametrize("n", [16500, 18000, 20400])
+def test_decode_two_static_super_tiles(dev, n):
+    """One sequence, 8 KV heads: 128 waves share the keys; between about 16.3k and 20.5k keys
+    each wave takes two super-tiles statically and its third from the tile counter (its first
+    dynamic one), so the counter must be read already for that third super-tile."""
+    from lagunalab_amd.q8_attn import decode_append_attention, q8_decode_attention
+    rng = np.random.default_rng(n)
+    Hkv, G = 8, 4
+    cap = (n + 256) // 256 * 256
+    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (1, Hkv * G, 1, 128))
+    got = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, n, 0.09)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"decode n={n}")
+    # the fused step at the same length: append row n - 1, attend over n rows
+    k1 = to_dev_bf16(Q.randn_bf16(rng, (1, Hkv, 1, 128)), dev)
+    v1 = to_dev_bf16(Q.randn_bf16(rng, (1, Hkv, 1, 128)), dev)
+    got = decode_append_attention(to_dev_bf16(q, dev), k1, v1, kq, vq, n=n - 1, scale=0.09)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"fused step n={n}")
+
+
 def test_decode_accepts_mlx_word_view_and_other_q_dtypes(dev):
     from lagunalab_amd.q8_attn import q8_decode_attention
     rng = np.random.default_rng(3)
