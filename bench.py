@@ -586,7 +586,8 @@ def main():
     # call is also timed that way and reported as attn_us_per_call.
     group = 8
     pairs, attn_n = [], []
-    for gi in range(max(1, args.roofline_calls // group)):
+    n_groups = args.roofline_calls // group if not args.separate_append else max(1, args.roofline_calls // group)
+    for gi in range(n_groups):
         e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         e[0].record(stream)
         for k in range(group):
@@ -597,15 +598,15 @@ def main():
         e[1].record(stream)
         pairs.append(e)
     torch.cuda.synchronize()
-    attn_ms = [a.elapsed_time(b) / group for a, b in pairs]
+    attn_ms = [a.elapsed_time(b) / group for a, b in pairs]  # empty with --roofline-calls 0
 
     # per step: K/V codes + scales/biases over n rows, the new bf16 K/V rows read (4096 B), the
     # appended q8 K/V rows written (2176 B), q read and out written (8192 B each)
     step_bytes = [Q8_TOKEN * n + 2 * HKV * D * 2 + Q8_TOKEN + 2 * HQ * D * 2 for n in ns]
     value = sum(step_bytes) / (total_ms * 1e-3) / 1e9
     attn_bytes = [Q8_TOKEN * n + 2 * HQ * D * 2 for n in attn_n]
-    attn_avg_ms = sum(attn_ms) / len(attn_ms)
-    attn_med_ms = sorted(attn_ms)[len(attn_ms) // 2]
+    attn_avg_ms = sum(attn_ms) / len(attn_ms) if attn_ms else None
+    attn_med_ms = sorted(attn_ms)[len(attn_ms) // 2] if attn_ms else None
     if args.separate_append:
         kernel = "lq_decode_attn (q8_attn_packed_kernel, split merge fused)"
         k_ms, k_bytes, k_calls = attn_avg_ms, sum(attn_bytes) / len(attn_bytes), len(attn_ms) * group
@@ -636,7 +637,8 @@ def main():
                    "ctx": ctx, "batch": 1, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "layers": nl, "cap": cap},
         "us_per_call": round(total_ms / args.steps * 1e3, 2),
-        "attn_us_per_call": {"mean": round(attn_avg_ms * 1e3, 2), "median": round(attn_med_ms * 1e3, 2)},
+        "attn_us_per_call": ({"mean": round(attn_avg_ms * 1e3, 2), "median": round(attn_med_ms * 1e3, 2)}
+                             if attn_ms else None),
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
