@@ -102,6 +102,20 @@ def test_workspace_queries(lib):
     assert lib.lq_accept_workspace_bytes(5, 131072) == 5 * 32 * 8
 
 
+def test_python_constants_match_header():
+    """The constants the Python side uses equal the header's #defines."""
+    import re
+    from pathlib import Path
+
+    from lagunalab_amd import _lib
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "laguna_hip.h").read_text()
+    defs = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (LQ_\w+) (\d+)", hdr)}
+    names = ("LQ_WS_ZERO_BYTES", "LQ_MAX_SEQS", "LQ_OK", "LQ_EINVAL", "LQ_EHIP", "LQ_EWORKSPACE",
+             "LQ_KV_Q8", "LQ_KV_Q4", "LQ_KV_BF16")
+    for name in names:
+        assert getattr(_lib, name) == defs[name], name
+
+
 def test_decode_split_plan_fills_one_wave(lib):
     """The 8-bit decode plan gives each KV head at most one wave of resident workgroups (256 CUs,
     one workgroup each, over 8 KV heads: 32 splits per head), apportioned over the sequences by
