@@ -95,6 +95,29 @@ class QuantizedKVCache:
         return (tuple(t[:, :, :self.offset] for t in self.keys),
                 tuple(t[:, :, :self.offset] for t in self.values))
 
+    @state.setter
+    def state(self, v):
+        """mlx-lm's setter: the ``(codes, scales, biases)`` tuples of the valid rows become the
+        buffers (contiguous copies) and ``offset`` their row count; the next append grows them."""
+        keys, values = v
+        if keys is None:
+            self.keys = self.values = None
+            self.offset = 0
+            return
+        self.keys = tuple(t.contiguous() for t in keys)
+        self.values = tuple(t.contiguous() for t in values)
+        self.offset = self.keys[0].shape[2]
+
+    @property
+    def meta_state(self):
+        return tuple(map(str, (self.step, self.offset, self.group_size, self.bits)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        step, self.offset, self.group_size, self.bits = map(int, v)
+        if step != self.step:
+            raise ValueError(f"saved step {step} differs from {self.step}")
+
     def make_mask(self, N, return_array=False, window_size=None):
         return create_attention_mask(N, offset=self.offset, return_array=return_array,
                                      window_size=window_size)
@@ -235,6 +258,26 @@ class DequantKVCache:
         self._flush()
         return self.q.state
 
+    @state.setter
+    def state(self, v):
+        """Extension: the reference class has no setter (``docs/architecture.md:347-349``), so its
+        prompt caches cannot be loaded; here the packed tuples load into the wrapped cache."""
+        self._pending = None
+        self._quantized_step = self.fused_step = False
+        self.q.state = v
+
+    @property
+    def meta_state(self):
+        return self.q.meta_state + tuple(
+            str(int(x)) for x in (self.quantized_decode, self.fused_decode, self.fused_verify))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.q.meta_state = v[:4]
+        self.quantized_decode, self.fused_decode, self.fused_verify = (bool(int(x)) for x in v[4:7])
+        if self.fused_decode and (self.q.bits, self.q.group_size) != (8, 64):
+            raise ValueError("fused_decode needs 8-bit, group_size 64")
+
     def is_trimmable(self):
         return True
 
@@ -293,7 +336,23 @@ class KVCache:
 
     @property
     def state(self):
+        if self.keys is None:
+            return None, None
         return self.keys[:, :, :self.offset], self.values[:, :, :self.offset]
+
+    @state.setter
+    def state(self, v):
+        self.keys, self.values = (None, None) if v[0] is None else (v[0].contiguous(), v[1].contiguous())
+        self.offset = 0 if self.keys is None else self.keys.shape[2]
+
+    @property
+    def meta_state(self):
+        return ()
+
+    @meta_state.setter
+    def meta_state(self, v):
+        if v:
+            raise ValueError("KVCache has no meta state")
 
     @property
     def nbytes(self):
@@ -330,6 +389,22 @@ class RotatingKVCache:
         return self.keys is None
 
     @property
+    def state(self):
+        return self.keys, self.values
+
+    @state.setter
+    def state(self, v):
+        self.keys, self.values = v
+
+    @property
+    def meta_state(self):
+        return tuple(map(str, (self.max_size, self.offset)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.max_size, self.offset = map(int, v)
+
+    @property
     def nbytes(self):
         return 0 if self.keys is None else self.keys.nbytes + self.values.nbytes
 
@@ -364,6 +439,18 @@ class TrimmableWindowCache:
     @property
     def state(self):
         return self.keys, self.values
+
+    @state.setter
+    def state(self, v):
+        self.keys, self.values = v
+
+    @property
+    def meta_state(self):
+        return tuple(map(str, (self.window, self.slack, self.offset)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.window, self.slack, self.offset = map(int, v)
 
     def is_trimmable(self):
         return True

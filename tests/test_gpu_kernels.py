@@ -589,6 +589,31 @@ def test_fused_step_cache_defers_and_flushes(dev):
     assert fused.trim(2) == 2 and fused.offset == 256
 
 
+def test_prompt_cache_round_trip_continues_decoding(dev, tmp_path):
+    """A fused-decode cache saved mid-step (a fused append still pending) and loaded again: the
+    file holds the appended row, and the next fused decode steps on the loaded cache give the
+    original cache's outputs and bytes bit for bit."""
+    from lagunalab_amd.cache import DequantKVCache
+    from lagunalab_amd.prompt_cache import load_prompt_cache, save_prompt_cache
+    rng = np.random.default_rng(12)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 8, L, 128)), dev)
+    a = DequantKVCache(fused_decode=True)
+    a.update_and_fetch(kv(700), kv(700))
+    a.update_and_fetch(kv(1), kv(1))  # pending: save() must write it first
+    f = tmp_path / "p.safetensors"
+    save_prompt_cache(f, [a], {"tokens": "701"})
+    (b,), meta = load_prompt_cache(f, device=dev, return_metadata=True)
+    assert meta == {"tokens": "701"} and b.offset == a.offset == 701 and b.fused_decode
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 1, 128)), dev)
+    for _ in range(3):
+        k1, v1 = kv(1), kv(1)
+        a.update_and_fetch(k1, v1)
+        b.update_and_fetch(k1, v1)
+        assert torch.equal(a.attend(q, 0.09), b.attend(q, 0.09))
+    for x, y in zip(a.state[0] + a.state[1], b.state[0] + b.state[1]):
+        assert torch.equal(x, y)
+
+
 # ---------------------------------------------------------------------------------------------
 # fused causal verify attention (speculative-decoding block)
 # ---------------------------------------------------------------------------------------------
