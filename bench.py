@@ -55,12 +55,13 @@ def parse():
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "q4", "bf16", "ragged", "verify", "lookup"],
+                   choices=["decode", "q4", "bf16", "ragged", "verify", "lookup", "layers"],
                    help="decode: the 8-bit decode step (default). q4 / bf16: decode attention over "
                         "a 4-bit / plain bf16 cache at the same context. ragged: 8 sequences of "
                         "default_rng(1) lengths in [42771, 82671]. verify: a 5-row causal verify "
                         "block over 65,536 cached rows plus its append. lookup: n-gram draft search "
-                        "over 82,671 ids and greedy accept of 5 x 131,072 logits")
+                        "over 82,671 ids and greedy accept of 5 x 131,072 logits. layers: one decoded "
+                        "token through the attention blocks of --layers full-attention layers")
     return p.parse_args()
 
 
@@ -402,6 +403,81 @@ def run_workload(args):
                 {"workload": f"append 5 rows + causal verify attention, {HQ}q/{HKV}kv heads, "
                              f"head_dim {D}, {nc} cached rows, {nl} rotating caches",
                  "q_len": L, "ctx": nc + L, "layers": nl}, extra)
+        return
+
+    if args.workload == "layers":
+        # One decoded token through the attention blocks of the model's full-attention layers
+        # (laguna.py:94-111 per layer; the residual add fused with the next input RMSNorm):
+        # projection GEMM for q/k/v/gate, q/k RMSNorm + RoPE (YaRN, partial rotary 0.5), the fused
+        # decode step over the layer's 8-bit cache, the softplus gate, o_proj GEMM. Synthetic bf16
+        # weights N(0, 0.02), caches of 82,671 quantized N(0,1) rows per layer. Timed as one HIP
+        # graph replay per token (positions on the device); the eager step is timed beside it.
+        from lagunalab_amd.attention import Attention
+        from lagunalab_amd.cache import DequantKVCache
+        from lagunalab_amd.decoder import DecodeStack
+        C, nl, n0 = 2048, args.layers, args.ctx
+        rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0,
+                "partial_rotary_factor": 0.5, "original_max_position_embeddings": 4096}
+        w = lambda *sh: (0.02 * torch.randn(sh, device=dev, generator=g)).to(torch.bfloat16)
+        blocks, caches, norms = [], [], []
+        for _ in range(nl):
+            blocks.append(Attention(w(HQ * D, C), w(HKV * D, C), w(HKV * D, C), w(C, HQ * D),
+                                    w(HQ, C), 1 + w(D), 1 + w(D), HQ, HKV, rope))
+            norms.append(1 + w(C))
+            c = DequantKVCache(fused_decode=True)
+            kx = torch.randn((1, HKV, n0, D), device=dev, generator=g).to(torch.bfloat16)
+            vx = torch.randn((1, HKV, n0, D), device=dev, generator=g).to(torch.bfloat16)
+            c.q.update_and_fetch(kx, vx)  # quantize the prefill rows (no dequantized copy)
+            del kx, vx
+            caches.append(c)
+        stack = DecodeStack(blocks, norms, caches)
+        n_eager = min(32, args.steps)
+        xs = torch.randn((2 * args.warmup + n_eager + args.steps, 1, 1, C), device=dev,
+                         generator=g).to(torch.bfloat16)
+        # eager steps (host-issued launches)
+        for j in range(args.warmup):
+            stack.step(xs[j])
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for j in range(n_eager):
+            stack.step(xs[args.warmup + j])
+        t1.record(stream)
+        torch.cuda.synchronize()
+        eager_ms = t0.elapsed_time(t1) / n_eager
+        # graph replays
+        stack.capture(args.warmup + args.steps)
+        base = args.warmup + n_eager
+        for j in range(args.warmup):
+            stack.replay(xs[base + j])
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for j in range(args.steps):
+            stack.replay(xs[base + args.warmup + j])
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        n_mid = n0 + args.warmup + n_eager + args.warmup + args.steps // 2
+        w_bytes = nl * 2 * (((HQ + 2 * HKV) * D + HQ) * C + C * HQ * D)  # q/k/v/gate + o_proj weights
+        kv_bytes = nl * (Q8_TOKEN * n_mid + 2 * HKV * D * 2 + Q8_TOKEN + 2 * HQ * D * 2)
+        nbytes = w_bytes + kv_bytes
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        extra = {"us_per_token": round(ms * 1e3, 1), "tokens_per_s": round(1e3 / ms, 1),
+                 "eager_us_per_token": round(eager_ms * 1e3, 1),
+                 "pct_of_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
+                 "bytes_per_token": {"kv": kv_bytes, "weights": w_bytes},
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                              "kernel": f"one HIP graph per token: {nl} x (lq_add_rms_norm, GEMM, "
+                                        "lq_qk_norm_rope, lq_q8_decode_append_attn_pos, "
+                                        "lq_gate_heads, GEMM)",
+                              "bytes_per_call": nbytes}}
+        _result(f"attention blocks of {nl} full-attention layers, us per decoded token at "
+                f"{n0}-token ctx", round(ms * 1e3, 2), "us/token", False, ms, args, "u8",
+                {"workload": f"decode token through {nl} full-attention blocks (hidden {C}, "
+                             f"{HQ}q/{HKV}kv heads, head_dim {D}, YaRN RoPE 0.5, per-head gate, "
+                             f"8-bit cache of {n0} rows each), one HIP graph per token",
+                 "ctx": n0, "layers": nl, "hidden": C}, extra)
         return
 
     if args.workload == "lookup":

@@ -185,6 +185,52 @@ int lq_greedy_accept(const float* logits, int64_t L, int64_t V, const int32_t* d
                      int64_t m, int32_t* out, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/*
+ * lq_q8_decode_append_attn with the append rows read on the device: pos int32 [B] (device) is the
+ * row each sequence appends at (its rows before the append), so that one recorded launch -- a HIP
+ * graph of a decode step -- serves every step; the split plan and the workspace are those of
+ * n_plan rows per sequence (size the workspace with lq_decode_workspace_bytes for n_plan + 1).
+ * Each sequence attends over min(pos[b] + 1, cap) rows; keep pos[b] < cap. At most 4 query heads
+ * per KV head.
+ */
+int lq_q8_decode_append_attn_pos(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                 uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc,
+                                 uint16_t* vs, uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv,
+                                 int64_t D, int64_t cap, int64_t n_plan, const int32_t* pos,
+                                 float scale, uint16_t* out, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
+/*
+ * q/k RMSNorm + RoPE of the attention block (laguna_mlx/laguna.py:97-101: q_norm / k_norm over
+ * head_dim, then rope at the cache offset; mlx-lm initialize_rope frequencies, passed in):
+ *   q bf16 [B, Hq, L, 128], k bf16 [B, Hkv, L, 128] -> q_out, k_out (same shapes; may alias)
+ *   q_norm_w, k_norm_w bf16 [128]; inv_freq fp32 [rot_dims / 2] (device): dim i < rot_dims / 2
+ *   pairs with i + rot_dims / 2 at angle (offset + l) * inv_freq[i] (offsets int32 [B], device,
+ *   per sequence when not null); mscale scales the rotated dims (YaRN); dims >= rot_dims pass.
+ * rot_dims a multiple of 4 in [0, 128].
+ */
+int lq_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
+                    const uint16_t* q_norm_w, const uint16_t* k_norm_w, int64_t B, int64_t Hq,
+                    int64_t Hkv, int64_t L, int64_t D, float eps, const float* inv_freq,
+                    int64_t rot_dims, float mscale, int64_t offset, const int32_t* offsets,
+                    void* stream);
+
+/*
+ * Output gate of the attention block (laguna_mlx/laguna.py:108-110):
+ *   out[b, l, h, :] = attn[b, h, l, :] * softplus(gate)   (bf16, o_proj's [B, L, Hq, 128] layout)
+ *   gate bf16 [B, L, Hq] (per-head gating) or [B, L, Hq, 128] (per_dim != 0)
+ */
+int lq_gate_heads(const uint16_t* attn, const uint16_t* gate, uint16_t* out, int64_t B,
+                  int64_t Hq, int64_t L, int64_t D, int per_dim, void* stream);
+
+/*
+ * Residual add + RMSNorm of a decoder layer's input (laguna.py's input_layernorm after the
+ * previous block's residual add): h_out = h + d (bf16; d may be null: no add, h_out unused),
+ * y = RMSNorm(h_out) * w (bf16), rows of C values, C a multiple of 8 up to 8192. h_out may alias h.
+ */
+int lq_add_rms_norm(const uint16_t* h, const uint16_t* d, const uint16_t* w, uint16_t* h_out,
+                    uint16_t* y, int64_t rows, int64_t C, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,12 @@ SIGNATURES = {
     "lq_ngram_propose": (i32, [vp, i64, i32, i32, vp, vp, i64, vp]),
     "lq_accept_workspace_bytes": (i64, [i64, i64]),
     "lq_greedy_accept": (i32, [vp, i64, i64, vp, i64, vp, vp, i64, vp]),
+    "lq_qk_norm_rope": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, f32, vp, i64, f32,
+                              i64, vp, vp]),
+    "lq_gate_heads": (i32, [vp, vp, vp, i64, i64, i64, i64, i32, vp]),
+    "lq_add_rms_norm": (i32, [vp, vp, vp, vp, vp, i64, i64, f32, vp]),
+    "lq_q8_decode_append_attn_pos": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
+                                           i64, i64, vp, f32, vp, vp, i64, vp]),
 }
 
 _lib = None

@@ -240,7 +240,7 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                 uint16_t* vs, uint16_t* vb, const uint16_t* k_new, const uint16_t* v_new,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                 const int32_t* lens, float scale, uint16_t* out, void* workspace,
-                int64_t workspace_bytes, hipStream_t st) {
+                int64_t workspace_bytes, hipStream_t st, const int32_t* pos_dev = nullptr) {
   LQ_CHECK_ARG(kind == LQ_KV_Q8 ||
                    ((kind == LQ_KV_BF16 || kind == LQ_KV_Q4) && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
                "kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
@@ -266,7 +266,10 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
     return LQ_EWORKSPACE;
   }
   const bool fused_merge = kind != LQ_KV_Q8 || attn_merges_itself(Hq / Hkv);
+  LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new && attn_merges_itself(Hq / Hkv)),
+               "device positions need the fused 8-bit append with at most 4 query heads per KV head");
   AttnArgs a{};
+  a.pos = pos_dev;
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);
   a.ks = ks;
@@ -342,4 +345,21 @@ extern "C" int lq_q8_decode_append_attn(const uint16_t* q, const uint16_t* k_new
   return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
                      n + 1, lens_host ? after : nullptr, scale, out, workspace, workspace_bytes,
                      (hipStream_t)stream);
+}
+
+extern "C" int lq_q8_decode_append_attn_pos(const uint16_t* q, const uint16_t* k_new,
+                                            const uint16_t* v_new, uint8_t* kc, uint16_t* ks,
+                                            uint16_t* kb, uint8_t* vc, uint16_t* vs, uint16_t* vb,
+                                            int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                            int64_t cap, int64_t n_plan, const int32_t* pos,
+                                            float scale, uint16_t* out, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(k_new && v_new && pos, "null pointer");
+  LQ_CHECK_ARG(n_plan >= 0 && n_plan < cap, "n_plan=%lld leaves no room to append in capacity %lld",
+               (long long)n_plan, (long long)cap);
+  return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
+                     n_plan + 1, nullptr, scale, out, workspace, workspace_bytes,
+                     (hipStream_t)stream, pos);
 }

@@ -1,0 +1,236 @@
+// The decoder-layer operations around the cache in the attention block of a full-attention layer
+// (laguna_mlx/laguna.py:94-111): q/k RMSNorm + RoPE at the cache offset before update_and_fetch,
+// and the softplus output gate after attention.
+//
+// lq_qk_norm_rope replaces q_norm/k_norm (nn.RMSNorm over head_dim, laguna.py:89-90,97-98) and
+// the rope calls (laguna.py:100-101; mlx-lm's initialize_rope: default or YaRN frequencies,
+// partial rotary): one wave per (head, row), lane l holding dims 2l and 2l + 1 (head_dim 128).
+// The normalized row is rounded to bf16 before the rotation, as the reference's two separate
+// ops round between them. The rotation is the non-interleaved form on the first `rot_dims` dims:
+// dim i pairs with dim i + rot_dims / 2, angle (position) * inv_freq[i]; the partner value sits
+// rot_dims / 4 lanes away. `mscale` (YaRN's attention factor) scales the rotated dims.
+//
+// lq_gate_heads replaces `out.transpose(0, 2, 1, 3) * softplus(g_proj(x))` (laguna.py:108-110):
+// the gate in fp32, rounded to bf16 like the reference's astype, the product rounded to bf16, and
+// the result written in o_proj's [B, L, Hq, D] layout (the transpose folded into the store).
+#include "common.h"
+
+namespace lq {
+namespace {
+
+constexpr int ND = 128;  // head_dim
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, const uint16_t* __restrict__ q_w,
+    const uint16_t* __restrict__ k_w, int64_t B, int Hq, int Hkv, int64_t L, float eps,
+    const float* __restrict__ inv_freq, int rot_dims, float mscale, int64_t offset,
+    const int32_t* __restrict__ offsets) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // over B (Hq + Hkv) L
+  const int64_t per_b = (int64_t)(Hq + Hkv) * L;
+  if (row >= B * per_b) return;  // wave-uniform
+  const int64_t b = row / per_b;
+  const int64_t r = row - b * per_b;
+  const bool is_q = r < (int64_t)Hq * L;
+  const int64_t hr = is_q ? r : r - (int64_t)Hq * L;  // head * L + l within q or k
+  const int64_t l = hr % L;
+  const int64_t src_row = (b * (is_q ? Hq : Hkv)) * L + hr;
+  const uint16_t* in = (is_q ? q : k) + src_row * ND;
+  uint16_t* out = (is_q ? q_out : k_out) + src_row * ND;
+  const uint16_t* w = is_q ? q_w : k_w;
+
+  const uint32_t x2 = reinterpret_cast<const uint32_t*>(in)[lane];
+  const uint32_t w2 = reinterpret_cast<const uint32_t*>(w)[lane];
+  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
+  float ss = x0 * x0 + x1 * x1;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const float inv = 1.0f / sqrtf(ss * (1.0f / ND) + eps);
+  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
+  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
+  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
+
+  const int half = rot_dims >> 1;      // rotated pairs
+  const int lane_off = rot_dims >> 2;  // partner lane distance
+  const bool rot = 2 * lane < rot_dims;
+  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
+  const float p0 = __shfl(y0, partner, 64);
+  const float p1 = __shfl(y1, partner, 64);
+  if (rot) {
+    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
+    const int i0 = first ? 2 * lane : 2 * lane - half;
+    const float pos = (float)((offsets ? (int64_t)offsets[b] : offset) + l);
+    float s0, c0, s1, c1;
+    sincosf(pos * inv_freq[i0], &s0, &c0);
+    sincosf(pos * inv_freq[i0 + 1], &s1, &c1);
+    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
+    if (first) {
+      y0 = a0 * c0 - b0 * s0;
+      y1 = a1 * c1 - b1 * s1;
+    } else {  // this lane holds x_{i+half}; the partner holds x_i
+      y0 = b0 * s0 + a0 * c0;
+      y1 = b1 * s1 + a1 * c1;
+    }
+  }
+  reinterpret_cast<uint32_t*>(out)[lane] =
+      (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+}
+
+// softplus(x) = log(1 + e^x), written as max(x, 0) + log1p(e^-|x|) (no overflow for large x)
+__device__ __forceinline__ float softplus_f(float x) { return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x))); }
+
+// One thread per 8 dims of one (b, h, l) row of attn [B, Hq, L, D]; gate g is [B, L, Hq] (per
+// head) or [B, L, Hq, D] (per dim).
+__global__ __launch_bounds__(256) void gate_heads_kernel(const uint16_t* __restrict__ attn,
+                                                         const uint16_t* __restrict__ g,
+                                                         uint16_t* __restrict__ out, int64_t B,
+                                                         int Hq, int64_t L, int per_dim) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = B * Hq * L * (ND / 8);
+  if (t >= total) return;
+  const int c = (int)(t % (ND / 8));
+  const int64_t rowi = t / (ND / 8);  // (b, h, l) in attn order
+  const int64_t l = rowi % L;
+  const int64_t bh = rowi / L;
+  const int h = (int)(bh % Hq);
+  const int64_t b = bh / Hq;
+  const uint4 a = reinterpret_cast<const uint4*>(attn + rowi * ND)[c];
+  const int64_t orow = (b * L + l) * Hq + h;  // row of out [B, L, Hq, D] and of a per-dim gate
+  uint32_t aw[4] = {a.x, a.y, a.z, a.w}, ow[4];
+  if (per_dim) {
+    const uint4 gv = reinterpret_cast<const uint4*>(g + orow * ND)[c];
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_lo(gw[j]))));
+      const float g1 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_hi(gw[j]))));
+      ow[j] = (uint32_t)f32_to_bf16(bf16_lo(aw[j]) * g0) |
+              ((uint32_t)f32_to_bf16(bf16_hi(aw[j]) * g1) << 16);
+    }
+  } else {
+    const float gate = bf16_to_f32(f32_to_bf16(softplus_f(bf16_to_f32(g[orow]))));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      ow[j] = (uint32_t)f32_to_bf16(bf16_lo(aw[j]) * gate) |
+              ((uint32_t)f32_to_bf16(bf16_hi(aw[j]) * gate) << 16);
+  }
+  reinterpret_cast<uint4*>(out + orow * ND)[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+// Residual add + RMSNorm over rows of C (<= 8192, multiple of 8) bf16 values, one workgroup per
+// row, 8 values per thread: h_out = bf16(h + d) (d may be null: h_out = h), y = bf16(rms(h_out) w).
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint16_t* h,
+                                                           const uint16_t* __restrict__ d,
+                                                           const uint16_t* __restrict__ w,
+                                                           uint16_t* h_out,  // may alias h
+                                                           uint16_t* __restrict__ y, int C,
+                                                           float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int chunks = C / 8;
+  float v[4][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = tid + 256 * it;
+    if (c < chunks) {
+      const uint4 a = reinterpret_cast<const uint4*>(h + row * C)[c];
+      uint4 bb = make_uint4(0u, 0u, 0u, 0u);
+      if (d) bb = reinterpret_cast<const uint4*>(d + row * C)[c];
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {bb.x, bb.y, bb.z, bb.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = d ? f32_to_bf16(bf16_lo(aw[j]) + bf16_lo(bw[j])) : (uint16_t)(aw[j] & 0xffffu);
+        const uint16_t hi = d ? f32_to_bf16(bf16_hi(aw[j]) + bf16_hi(bw[j])) : (uint16_t)(aw[j] >> 16);
+        v[it][2 * j] = bf16_to_f32(lo);
+        v[it][2 * j + 1] = bf16_to_f32(hi);
+        ow[j] = (uint32_t)lo | ((uint32_t)hi << 16);
+        ss += v[it][2 * j] * v[it][2 * j] + v[it][2 * j + 1] * v[it][2 * j + 1];
+      }
+      if (d) reinterpret_cast<uint4*>(h_out + row * C)[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)C + eps);
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = tid + 256 * it;
+    if (c < chunks) {
+      const uint4 wv = reinterpret_cast<const uint4*>(w)[c];
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ow[j] = (uint32_t)f32_to_bf16(v[it][2 * j] * inv * bf16_lo(ww[j])) |
+                ((uint32_t)f32_to_bf16(v[it][2 * j + 1] * inv * bf16_hi(ww[j])) << 16);
+      reinterpret_cast<uint4*>(y + row * C)[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace lq
+
+extern "C" int lq_add_rms_norm(const uint16_t* h, const uint16_t* d, const uint16_t* w,
+                               uint16_t* h_out, uint16_t* y, int64_t rows, int64_t C, float eps,
+                               void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(C >= 8 && C <= 8192 && C % 8 == 0, "row size %lld must be a multiple of 8 in "
+               "[8, 8192]", (long long)C);
+  LQ_CHECK_ARG(rows >= 1 && rows <= INT32_MAX, "bad row count %lld", (long long)rows);
+  LQ_CHECK_ARG(h && w && y && (!d || h_out), "null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  add_rms_norm_kernel<<<dim3((unsigned)rows), dim3(256), 0, st>>>(h, d, w, h_out, y, (int)C, eps);
+  LQ_CHECK_LAUNCH("add_rms_norm_kernel");
+  return LQ_OK;
+}
+
+extern "C" int lq_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
+                               uint16_t* k_out, const uint16_t* q_norm_w,
+                               const uint16_t* k_norm_w, int64_t B, int64_t Hq, int64_t Hkv,
+                               int64_t L, int64_t D, float eps, const float* inv_freq,
+                               int64_t rot_dims, float mscale, int64_t offset,
+                               const int32_t* offsets, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(D == ND, "head_dim must be 128 (got %lld)", (long long)D);
+  LQ_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && L >= 1 && Hq <= 1024 && Hkv <= 1024,
+               "bad shape B=%lld Hq=%lld Hkv=%lld L=%lld", (long long)B, (long long)Hq,
+               (long long)Hkv, (long long)L);
+  LQ_CHECK_ARG(rot_dims >= 0 && rot_dims <= D && rot_dims % 4 == 0,
+               "rot_dims must be a multiple of 4 in [0, 128] (got %lld)", (long long)rot_dims);
+  LQ_CHECK_ARG(offset >= 0, "negative offset");
+  LQ_CHECK_ARG(q && k && q_out && k_out && q_norm_w && k_norm_w && (inv_freq || rot_dims == 0),
+               "null pointer");
+  const int64_t rows = B * (Hq + Hkv) * L;
+  LQ_CHECK_ARG(rows / 4 < (int64_t)INT32_MAX, "too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  qk_norm_rope_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st>>>(
+      q, k, q_out, k_out, q_norm_w, k_norm_w, B, (int)Hq, (int)Hkv, L, eps, inv_freq,
+      (int)rot_dims, mscale, offset, offsets);
+  LQ_CHECK_LAUNCH("qk_norm_rope_kernel");
+  return LQ_OK;
+}
+
+extern "C" int lq_gate_heads(const uint16_t* attn, const uint16_t* gate, uint16_t* out, int64_t B,
+                             int64_t Hq, int64_t L, int64_t D, int per_dim, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(D == ND, "head_dim must be 128 (got %lld)", (long long)D);
+  LQ_CHECK_ARG(B >= 1 && Hq >= 1 && L >= 1, "bad shape");
+  LQ_CHECK_ARG(attn && gate && out && attn != out, "null or aliased pointer");
+  const int64_t total = B * Hq * L * (ND / 8);
+  LQ_CHECK_ARG(total / 256 < (int64_t)INT32_MAX, "too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  gate_heads_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
+      attn, gate, out, B, (int)Hq, L, per_dim ? 1 : 0);
+  LQ_CHECK_LAUNCH("gate_heads_kernel");
+  return LQ_OK;
+}

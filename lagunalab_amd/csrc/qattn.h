@@ -38,6 +38,10 @@ struct AttnArgs {
   // len - 1 of each sequence; the kernel quantizes them, attends over them and stores them.
   const uint16_t* knew;
   const uint16_t* vnew;
+  // Device positions (packed kernel with the fused append only; null otherwise): int32 [B], the
+  // row sequence b appends at; its length is then pos[b] + 1 (clamped to [1, cap]) instead of
+  // the plan's len[b], so that a launch recorded in a HIP graph serves every decode step.
+  const int32_t* pos;
   float* part_acc;    // workspace: split partials
   float2* part_ml;
   uint32_t* counters; // workspace: arrival and tile counters (zero between calls)

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
   const int hk = blockIdx.y;
   int b;
   find_seq(plan, x, b);
-  const int n = plan.len[b];
+  const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap) : plan.len[b];
   // Work in super-tiles of PST keys. The NWS waves of the sequence's workgroups take about 80%
   // of them statically (wave gw: super-tiles gw + k NWS for k < NS), the rest one at a time from
   // the (sequence, KV head) tile counter, two super-tiles ahead. Waves that started late or sit

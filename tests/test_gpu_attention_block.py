@@ -1,0 +1,245 @@
+"""GPU parity of the attention block around the cache (``lagunalab_amd/attention.py``,
+``csrc/layer.hip``) against a float32 torch restatement of ``laguna_mlx/laguna.py:94-111`` with
+the reference's bf16 rounding points (norm output, rope output, gate, gated output).
+
+* ``lq_qk_norm_rope`` and ``lq_gate_heads``: within one bf16 rounding step of the restatement
+  (the two sides' rsqrt / sin / cos / exp / log1p may differ in the last fp32 bit).
+* The whole block over a quantized cache: prefill through the unfused path, decode steps and a
+  verify block through the fused kernels, against the restatement over the same cache with the
+  unfused path throughout; the gap is the fused-vs-unfused attention difference carried through
+  the gate and o_proj.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+BF16_ULP = 2.0 ** -7  # relative spacing of bf16 around 1
+
+
+def _bf16(rng, shape, s=1.0, dev="cuda"):
+    return torch.from_numpy((s * rng.standard_normal(shape)).astype(np.float32)).to(dev).to(torch.bfloat16)
+
+
+def ref_norm_rope(x, w, eps, inv, rot, mscale, pos0):
+    """x bf16 [B, H, L, D]; pos0: int or int tensor [B]."""
+    B, H, L, D = x.shape
+    xf = x.float()
+    y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(torch.bfloat16).float()
+    if rot:
+        h = rot // 2
+        p0 = torch.as_tensor(pos0, device=x.device).reshape(-1, 1, 1).float()
+        pos = (p0 + torch.arange(L, device=x.device).float()[None, :, None]).expand(B, L, 1)
+        ang = (pos * inv.to(x.device)[None, None, :])[:, None]  # [B, 1, L, h]
+        c, s = ang.cos(), ang.sin()
+        a, b = y[..., :h] * mscale, y[..., h:rot] * mscale
+        y = torch.cat([a * c - b * s, a * s + b * c, y[..., rot:]], dim=-1)
+    return y.to(torch.bfloat16)
+
+
+def assert_within_ulp(got, want, what):
+    g, w = got.float(), want.float()
+    bad = (g - w).abs() > BF16_ULP * w.abs() + 1e-30
+    assert int(bad.sum()) == 0, f"{what}: {int(bad.sum())} elements beyond one bf16 step, max " \
+                                f"{float((g - w).abs().max())}"
+
+
+@pytest.mark.parametrize("case", ["full", "partial_yarn", "norm_only"])
+def test_qk_norm_rope_matches_restatement(dev, case):
+    from lagunalab_amd import _lib
+    from lagunalab_amd.attention import rope_frequencies
+    rng = np.random.default_rng({"full": 1, "partial_yarn": 2, "norm_only": 3}[case])
+    if case == "full":
+        B, Hq, Hkv, L, rope, offsets = 1, 32, 8, 1, {"rope_theta": 1e4}, 82671
+    elif case == "partial_yarn":
+        B, Hq, Hkv, L = 2, 48, 8, 5
+        rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0, "partial_rotary_factor": 0.5,
+                "original_max_position_embeddings": 4096}
+        offsets = torch.tensor([100, 65536], dtype=torch.int32, device=dev)
+    else:
+        B, Hq, Hkv, L, rope, offsets = 1, 4, 1, 3, {"rope_theta": 1e4, "partial_rotary_factor": 0.0}, 7
+    inv, rot, ms = rope_frequencies(128, rope)
+    inv = inv.to(dev)
+    q, k = _bf16(rng, (B, Hq, L, 128), 3.0), _bf16(rng, (B, Hkv, L, 128), 0.5)
+    wq, wk = _bf16(rng, (128,), 0.2) + 1, _bf16(rng, (128,), 0.2) + 1
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    lib = _lib.load()
+    off_t = offsets if torch.is_tensor(offsets) else None
+    off_s = 0 if torch.is_tensor(offsets) else offsets
+    st = lib.lq_qk_norm_rope(q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), wq.data_ptr(),
+                             wk.data_ptr(), B, Hq, Hkv, L, 128, 1e-6,
+                             inv.data_ptr() if rot else None, rot, ms, off_s,
+                             off_t.data_ptr() if off_t is not None else None,
+                             _lib.stream_ptr(dev))
+    _lib.check(st, "lq_qk_norm_rope")
+    pos0 = offsets if torch.is_tensor(offsets) else offsets
+    assert_within_ulp(qo, ref_norm_rope(q, wq, 1e-6, inv, rot, ms, pos0), f"q {case}")
+    assert_within_ulp(ko, ref_norm_rope(k, wk, 1e-6, inv, rot, ms, pos0), f"k {case}")
+    # in place gives the same bytes
+    q2, k2 = q.clone(), k.clone()
+    _lib.check(lib.lq_qk_norm_rope(q2.data_ptr(), k2.data_ptr(), q2.data_ptr(), k2.data_ptr(),
+                                   wq.data_ptr(), wk.data_ptr(), B, Hq, Hkv, L, 128, 1e-6,
+                                   inv.data_ptr() if rot else None, rot, ms, off_s,
+                                   off_t.data_ptr() if off_t is not None else None,
+                                   _lib.stream_ptr(dev)), "in place")
+    assert torch.equal(q2, qo) and torch.equal(k2, ko)
+
+
+@pytest.mark.parametrize("per_dim", [0, 1])
+def test_gate_heads_matches_restatement(dev, per_dim):
+    from lagunalab_amd import _lib
+    rng = np.random.default_rng(3 + per_dim)
+    B, H, L = 2, 32, 5
+    attn = _bf16(rng, (B, H, L, 128))
+    g = _bf16(rng, (B, L, H, 128) if per_dim else (B, L, H), 4.0)
+    out = torch.empty((B, L, H, 128), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.load().lq_gate_heads(attn.data_ptr(), g.data_ptr(), out.data_ptr(), B, H, L, 128,
+                                         per_dim, _lib.stream_ptr(dev)), "lq_gate_heads")
+    gate = torch.nn.functional.softplus(g.float()).to(torch.bfloat16)
+    gate = gate if per_dim else gate[..., None]
+    want = (attn.transpose(1, 2).float() * gate.float()).to(torch.bfloat16)
+    assert_within_ulp(out, want, f"gate per_dim={per_dim}")
+
+
+class RefBlock:
+    """laguna.py:94-111 in torch float32 with bf16 rounding points, unfused attention."""
+
+    def __init__(self, blk, rope):
+        from lagunalab_amd.attention import rope_frequencies
+        self.b = blk
+        self.inv, self.rot, self.ms = rope_frequencies(128, rope)
+
+    def __call__(self, x, mask, cache):
+        from lagunalab_amd.attention import _sdpa
+        b = self.b
+        B, L, _ = x.shape
+        H, Hkv, D = b.n_heads, b.n_kv_heads, 128
+        wq, wk, wv, wg = torch.split(b.w_in, b._splits, dim=0)
+        q = torch.matmul(x, wq.t()).reshape(B, L, H, D).transpose(1, 2).contiguous()
+        k = torch.matmul(x, wk.t()).reshape(B, L, Hkv, D).transpose(1, 2).contiguous()
+        v = torch.matmul(x, wv.t()).reshape(B, L, Hkv, D).transpose(1, 2).contiguous()
+        g = torch.matmul(x, wg.t())
+        off = cache.offset
+        q = ref_norm_rope(q, b.q_norm, b.eps, self.inv, self.rot, self.ms, off)
+        k = ref_norm_rope(k, b.k_norm, b.eps, self.inv, self.rot, self.ms, off)
+        k, v = cache.update_and_fetch(k, v)
+        out = _sdpa(q, k, v, mask, b.scale).to(torch.bfloat16)
+        gate = torch.nn.functional.softplus(g.float()).to(torch.bfloat16)[..., None]
+        y = (out.transpose(1, 2).float() * gate.float()).to(torch.bfloat16)
+        return torch.matmul(y.reshape(B, L, H * D), b.wo.t())
+
+
+def test_attention_block_prefill_decode_verify(dev):
+    from lagunalab_amd.attention import Attention
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(11)
+    C, H, Hkv, D = 512, 8, 2, 128
+    rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0, "partial_rotary_factor": 0.5,
+            "original_max_position_embeddings": 4096}
+    w = lambda *s: _bf16(rng, s, 0.05)
+    blk = Attention(w(H * D, C), w(Hkv * D, C), w(Hkv * D, C), w(C, H * D), w(H, C),
+                    _bf16(rng, (D,), 0.1) + 1, _bf16(rng, (D,), 0.1) + 1, H, Hkv, rope)
+    ref = RefBlock(blk, rope)
+    fused, plain = DequantKVCache(fused_decode=True), DequantKVCache()
+    for L in (300, 1, 1, 1, 5, 1):
+        x = _bf16(rng, (1, L, C))
+        a = blk(x, fused.make_mask(L), fused)
+        want = ref(x, plain.make_mask(L), plain)
+        assert fused.fused_step == (L <= 16) and fused.offset == plain.offset
+        err = float((a.float() - want.float()).abs().max())
+        scale = float(want.float().abs().max())
+        assert err <= 2e-2 * scale, (L, err, scale)
+
+
+def test_add_rms_norm_matches_restatement(dev):
+    from lagunalab_amd.decoder import add_rms_norm
+    rng = np.random.default_rng(21)
+    for rows, C in ((1, 2048), (3, 512), (2, 8)):
+        h, d, w = _bf16(rng, (rows, C)), _bf16(rng, (rows, C)), _bf16(rng, (C,), 0.2) + 1
+        h0 = h.clone()
+        y = add_rms_norm(h, d, w, 1e-6)
+        s = (h0.float() + d.float()).to(torch.bfloat16)
+        assert torch.equal(h, s), (rows, C)  # the residual sum, one bf16 rounding
+        sf = s.float()
+        want = (sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()).to(torch.bfloat16)
+        assert_within_ulp(y, want, f"rms {rows}x{C}")
+        y2 = add_rms_norm(s.clone(), None, w, 1e-6)  # no residual
+        assert torch.equal(y2, y)
+
+
+def _stack(dev, seed, n0, layers=3, C=512, H=8, Hkv=2):
+    from lagunalab_amd.attention import Attention
+    from lagunalab_amd.cache import DequantKVCache
+    from lagunalab_amd.decoder import DecodeStack
+    rng = np.random.default_rng(seed)
+    rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0, "partial_rotary_factor": 0.5,
+            "original_max_position_embeddings": 4096}
+    w = lambda *s: _bf16(rng, s, 0.05)
+    blocks, norms, caches = [], [], []
+    for _ in range(layers):
+        blocks.append(Attention(w(H * 128, C), w(Hkv * 128, C), w(Hkv * 128, C), w(C, H * 128),
+                                w(H, C), _bf16(rng, (128,), 0.1) + 1, _bf16(rng, (128,), 0.1) + 1,
+                                H, Hkv, rope))
+        norms.append(_bf16(rng, (C,), 0.1) + 1)
+        c = DequantKVCache(fused_decode=True)
+        c.q.update_and_fetch(_bf16(rng, (1, Hkv, n0, 128)), _bf16(rng, (1, Hkv, n0, 128)))
+        caches.append(c)
+    return DecodeStack(blocks, norms, caches)
+
+
+def test_decode_pos_entry_matches_host_length(dev):
+    """lq_q8_decode_append_attn_pos (append row read on the device) equals
+    lq_q8_decode_append_attn (host n) bit for bit: output and cache bytes."""
+    from lagunalab_amd import _lib
+    from lagunalab_amd.q8_attn import decode_append_attention
+    from lagunalab_amd.quant import quantize_kv_into
+    rng = np.random.default_rng(31)
+    n, cap, Hkv = 5000, 5376, 8
+    k = _bf16(rng, (1, Hkv, n, 128))
+    v = _bf16(rng, (1, Hkv, n, 128))
+    mk = lambda: tuple(torch.zeros(s, dtype=dt, device=dev) for s, dt in (
+        ((1, Hkv, cap, 128), torch.uint8), ((1, Hkv, cap, 2), torch.bfloat16), ((1, Hkv, cap, 2), torch.bfloat16)))
+    ka, va = mk(), mk()
+    quantize_kv_into(k, v, ka, va, 0)
+    kb_, vb_ = tuple(t.clone() for t in ka), tuple(t.clone() for t in va)
+    lib = _lib.load()
+    pos = torch.tensor([n], dtype=torch.int32, device=dev)
+    nb = lib.lq_decode_workspace_bytes(8, 1, 32, Hkv, 128, n + 1, None)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    for step in range(3):
+        q = _bf16(rng, (1, 32, 1, 128))
+        k1, v1 = _bf16(rng, (1, Hkv, 1, 128)), _bf16(rng, (1, Hkv, 1, 128))
+        want = decode_append_attention(q, k1, v1, ka, va, n=n + step, scale=0.09)
+        got = torch.empty_like(want)
+        (kc, ks, kb), (vc, vs, vb) = kb_, vb_
+        _lib.check(lib.lq_q8_decode_append_attn_pos(
+            q.data_ptr(), k1.data_ptr(), v1.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+            vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, 32, Hkv, 128, cap, n, pos.data_ptr(),
+            0.09, got.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev)), "pos entry")
+        pos.add_(1)
+        assert torch.equal(got, want), step
+        for x, y in zip(ka + va, kb_ + vb_):
+            assert torch.equal(x, y), step
+
+
+def test_graph_step_matches_eager(dev):
+    """The decode step recorded in a HIP graph (positions on the device) gives the eager step's
+    residual stream bit for bit on every replay, with eager GPU work and synchronizations between
+    the replays, and leaves the caches with the same bytes."""
+    a, b = _stack(dev, 41, 4200), _stack(dev, 41, 4200)
+    b.capture(steps=6)
+    rng = np.random.default_rng(42)
+    for t in range(6):
+        x = _bf16(rng, (1, 1, 512))
+        want = a.step(x)
+        got = b.replay(x).clone()
+        assert torch.equal(got, want), t
+        torch.matmul(_bf16(rng, (64, 64)), _bf16(rng, (64, 64)))  # unrelated eager work
+        torch.cuda.synchronize()
+    for ca, cb in zip(a.caches, b.caches):
+        assert ca.offset == cb.offset == 4206
+        for x, y in zip(ca.state[0] + ca.state[1], cb.state[0] + cb.state[1]):
+            assert torch.equal(x, y)
+    with pytest.raises(RuntimeError, match="used up"):
+        b.replay(x)
