@@ -231,6 +231,13 @@ int lq_gate_heads(const uint16_t* attn, const uint16_t* gate, uint16_t* out, int
 int lq_add_rms_norm(const uint16_t* h, const uint16_t* d, const uint16_t* w, uint16_t* h_out,
                     uint16_t* y, int64_t rows, int64_t C, float eps, void* stream);
 
+/*
+ * y = W x for one input row (the projections of a decode step, laguna.py:97-99,110 at L = 1):
+ * W bf16 [N, K] row-major, x bf16 [K], y bf16 [N]; fp32 accumulation; K a multiple of 8.
+ */
+int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N, int64_t K,
+                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,8 +5,9 @@
 ``cache.offset``, ``update_and_fetch``, then ``cache.attend`` on fused steps or SDPA over the
 returned K/V otherwise, then the softplus output gate and ``o_proj``. The pieces:
 
-* one GEMM for q, k, v and the gate logits (the four projection weights concatenated; hipBLASLt
-  through torch), one for ``o_proj``;
+* one GEMM for q, k, v and the gate logits (the four projection weights concatenated), one for
+  ``o_proj``: ``lq_gemv_bf16`` for a single row (a decode step), hipBLASLt through torch for
+  more rows;
 * ``lq_qk_norm_rope``: the q and k RMSNorms and the rotary embedding of both in one launch
   (frequencies from :func:`rope_frequencies`: mlx-lm's default or YaRN RoPE, partial rotary);
 * the cache: the fused decode / verify kernels, or dequantized K/V for the unfused path;
@@ -83,6 +84,21 @@ def _sdpa(q, k, v, mask, scale):
     return torch.matmul(p, v.float()).reshape(B, Hq, Lq, D).to(q.dtype)
 
 
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``x @ w.T`` for bf16 ``x [..., K]`` and ``w [N, K]``: one row (a decode step) runs
+    ``lq_gemv_bf16`` (weight-streaming, HBM-bound), more rows the library GEMM."""
+    K = x.shape[-1]
+    if x.numel() != K:
+        return torch.matmul(x, w.t())
+    lib = _lib.load()
+    dev = _lib.require_device(x, w)
+    x = x.contiguous()
+    y = torch.empty((*x.shape[:-1], w.shape[0]), dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.lq_gemv_bf16(w.data_ptr(), x.data_ptr(), y.data_ptr(), w.shape[0], K,
+                                _lib.stream_ptr(dev)), "lq_gemv_bf16")
+    return y
+
+
 class Attention:
     """``laguna_mlx.laguna.Attention`` for a full-attention layer, head_dim 128.
 
@@ -112,7 +128,7 @@ class Attention:
         B, L, _ = x.shape
         H, Hkv, D = self.n_heads, self.n_kv_heads, self.head_dim
         x = x.to(torch.bfloat16)
-        proj = torch.matmul(x, self.w_in.t())  # [B, L, (H + 2 Hkv) D + gate]
+        proj = linear(x, self.w_in)  # [B, L, (H + 2 Hkv) D + gate]
         qp, kp, vp, gp = torch.split(proj, self._splits, dim=-1)
         q = qp.reshape(B, L, H, D).transpose(1, 2).contiguous()
         k = kp.reshape(B, L, Hkv, D).transpose(1, 2).contiguous()
@@ -135,4 +151,4 @@ class Attention:
         _lib.check(lib.lq_gate_heads(out.data_ptr(), g.data_ptr(), y.data_ptr(), B, H, L, D,
                                      0 if self.per_head_gate else 1, _lib.stream_ptr(dev)),
                    "lq_gate_heads")
-        return torch.matmul(y.reshape(B, L, H * D), self.wo.t())
+        return linear(y.reshape(B, L, H * D), self.wo)

@@ -174,8 +174,71 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint16_t* h,
   }
 }
 
+// y[n] = W[n, :] . x for one input row (the projections of a decode step): weights bf16 [N, K]
+// row-major, read once with 16-byte loads (HBM-bound); each wave takes RPW consecutive rows, lane
+// l the 8-element chunks l, l + 64, ... of each, fp32 products and sums, a wave reduction, bf16
+// out. K a multiple of 8.
+template <int RPW>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restrict__ W,
+                                                        const uint16_t* __restrict__ x,
+                                                        uint16_t* __restrict__ y, int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (r0 >= N) return;  // wave-uniform
+  const int chunks = K >> 3;
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+#pragma unroll 4
+  for (int c = lane; c < chunks; c += 64) {
+    const uint4 xv = reinterpret_cast<const uint4*>(x)[c];
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int row = min(r0 + r, N - 1);  // rows past N repeat the last one; not written
+      const uint4 wv = reinterpret_cast<const uint4*>(W + (int64_t)row * K)[c];
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      float a = acc[r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a = fmaf(bf16_lo(ww[j]), bf16_lo(xw[j]), a);
+        a = fmaf(bf16_hi(ww[j]), bf16_hi(xw[j]), a);
+      }
+      acc[r] = a;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float a = acc[r];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
+    if (lane == r && r0 + r < N) y[r0 + r] = f32_to_bf16(a);
+  }
+}
+
 }  // namespace
 }  // namespace lq
+
+extern "C" int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N,
+                            int64_t K, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(N >= 1 && N <= (1 << 26) && K >= 8 && K <= (1 << 20) && K % 8 == 0,
+               "bad GEMV shape N=%lld K=%lld (K a multiple of 8)", (long long)N, (long long)K);
+  LQ_CHECK_ARG(W && x && y, "null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  // two rows per wave once there are enough rows to fill the chip with them
+  if (N >= 4 * 2 * 2 * device_cu_count()) {
+    const int64_t waves = (N + 1) / 2;
+    gemv_bf16_kernel<2><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(W, x, y, (int)N,
+                                                                                  (int)K);
+  } else {
+    gemv_bf16_kernel<1><<<dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st>>>(W, x, y, (int)N,
+                                                                              (int)K);
+  }
+  LQ_CHECK_LAUNCH("gemv_bf16_kernel");
+  return LQ_OK;
+}
 
 extern "C" int lq_add_rms_norm(const uint16_t* h, const uint16_t* d, const uint16_t* w,
                                uint16_t* h_out, uint16_t* y, int64_t rows, int64_t C, float eps,

@@ -20,7 +20,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .attention import Attention
+from .attention import Attention, linear
 from .cache import DequantKVCache
 
 
@@ -65,7 +65,7 @@ class DecodeStack:
         dev = y.device
         sp = _lib.stream_ptr(dev)
         H, Hkv, D = blk.n_heads, blk.n_kv_heads, blk.head_dim
-        proj = torch.matmul(y, blk.w_in.t())  # [1, 1, (H + 2 Hkv) D + gate]
+        proj = linear(y, blk.w_in)  # [1, 1, (H + 2 Hkv) D + gate]
         q, k, v, g = torch.split(proj, blk._splits, dim=-1)  # contiguous pieces of one row
         _lib.check(lib.lq_qk_norm_rope(q.data_ptr(), k.data_ptr(), q.data_ptr(), k.data_ptr(),
                                        blk.q_norm.data_ptr(), blk.k_norm.data_ptr(), 1, H, Hkv, 1,
@@ -82,7 +82,7 @@ class DecodeStack:
         gated = torch.empty((1, 1, H, D), dtype=torch.bfloat16, device=dev)
         _lib.check(lib.lq_gate_heads(out.data_ptr(), g.data_ptr(), gated.data_ptr(), 1, H, 1, D,
                                      0 if blk.per_head_gate else 1, sp), "lq_gate_heads")
-        return torch.matmul(gated.reshape(1, 1, H * D), blk.wo.t())
+        return linear(gated.reshape(1, 1, H * D), blk.wo)
 
     def _step_pos(self):
         h, d = self.x_in.clone(), None

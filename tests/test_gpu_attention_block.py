@@ -152,6 +152,19 @@ def test_attention_block_prefill_decode_verify(dev):
         assert err <= 2e-2 * scale, (L, err, scale)
 
 
+@pytest.mark.parametrize("N,K", [(6176, 2048), (2048, 4096), (5, 8), (1, 520), (4099, 64)])
+def test_gemv_matches_float64(dev, N, K):
+    """lq_gemv_bf16 against float64 products of the same bf16 values: within the fp32
+    accumulation error plus one bf16 rounding of the result."""
+    from lagunalab_amd.attention import linear
+    rng = np.random.default_rng(N + K)
+    w, x = _bf16(rng, (N, K), 0.05), _bf16(rng, (1, 1, K))
+    y = linear(x, w)
+    want = (w.double() @ x.double().reshape(K)).reshape(1, 1, N)
+    bound = BF16_ULP * want.abs() + 1e-5 * (w.double().abs() @ x.double().abs().reshape(K)).reshape(1, 1, N)
+    assert y.shape == (1, 1, N) and bool(((y.double() - want).abs() <= bound).all())
+
+
 def test_add_rms_norm_matches_restatement(dev):
     from lagunalab_amd.decoder import add_rms_norm
     rng = np.random.default_rng(21)
