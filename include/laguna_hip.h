@@ -238,6 +238,19 @@ int lq_add_rms_norm(const uint16_t* h, const uint16_t* d, const uint16_t* w, uin
 int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N, int64_t K,
                  void* stream);
 
+/*
+ * The projections of a decode step with their neighbours fused in (one input row, W bf16 [N, K],
+ * K a multiple of 8 up to 4096):
+ *   mode 1 (input projection): y = W (RMSNorm(x) * aux), x the residual stream [K], aux the
+ *          layer's input-norm weights [K] (the norm's output rounded to bf16 as in the reference);
+ *   mode 2 (output projection): y = W (x * softplus(aux)), x the attention output [K = H * 128],
+ *          aux the gate logits [H] (per head) or [K] (per_dim != 0), gate and product in bf16;
+ *   res (may be null or equal y): y[n] = res[n] + (W . x)[n] in bf16, the residual add.
+ */
+int lq_gemv_fused(const uint16_t* W, const uint16_t* x, const uint16_t* aux, const uint16_t* res,
+                  uint16_t* y, int64_t N, int64_t K, int mode, float eps, int per_dim,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

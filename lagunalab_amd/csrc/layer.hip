@@ -216,8 +216,174 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restri
   }
 }
 
+// Input value chunk c of the fused GEMV (8 bf16 in four words), from the raw chunk xw.
+template <int IN>
+__device__ __forceinline__ void gemv_input(uint32_t (&xw)[4], const uint16_t* __restrict__ aux,
+                                           int c, float inv, int per_dim) {
+  if (IN == 1) {
+    const uint4 wn = reinterpret_cast<const uint4*>(aux)[c];
+    const uint32_t nw[4] = {wn.x, wn.y, wn.z, wn.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * inv * bf16_lo(nw[j])) |
+              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * inv * bf16_hi(nw[j])) << 16);
+  } else if (per_dim) {
+    const uint4 gv = reinterpret_cast<const uint4*>(aux)[c];
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_lo(gw[j]))));
+      const float g1 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_hi(gw[j]))));
+      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * g0) |
+              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * g1) << 16);
+    }
+  } else {
+    const float gate = bf16_to_f32(f32_to_bf16(softplus_f(bf16_to_f32(aux[(8 * c) / ND]))));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * gate) |
+              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * gate) << 16);
+  }
+}
+
+// a + w . x over the 8 bf16 of one chunk
+__device__ __forceinline__ float dot8(const uint4 w, const uint32_t (&xw)[4], float a) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a = fmaf(bf16_lo(ww[j]), bf16_lo(xw[j]), a);
+    a = fmaf(bf16_hi(ww[j]), bf16_hi(xw[j]), a);
+  }
+  return a;
+}
+
+// The two projections of a decode step with their neighbours fused in (one input row):
+//  * IN == 1 (input projection): x = RMSNorm(h) * w_in, the layer's input norm, each value
+//    rounded to bf16 as the separate norm would;
+//  * IN == 2 (output projection): x[k] = attn[k] * gate of k's head (softplus of the gate logit,
+//    rounded to bf16; per head or per dim), rounded to bf16 -- the gated attention output;
+//  * with `res`: y[n] = bf16(res[n] + bf16(W[n] . x)), the residual add (y may alias res).
+// Every wave first issues all its weight loads (lane l owns chunks l + 64 i, i < MAXC; K <= 512
+// MAXC), then the workgroup builds the input vector once into LDS (the norm's sum of squares
+// reduced over the workgroup), and each wave takes it from there.
+constexpr int MAXC = 8;
+template <int RPW, int IN>
+__global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* __restrict__ W,
+                                                         const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ aux,
+                                                         const uint16_t* res, uint16_t* y, int N,
+                                                         int K, float eps, int per_dim) {
+  __shared__ uint4 xs[64 * MAXC];
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int r0 = (blockIdx.x * 4 + (tid >> 6)) * RPW;
+  const bool live = r0 < N;  // wave-uniform; every wave joins the barriers below
+  const int chunks = K >> 3;
+  uint4 wreg[RPW][MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = lane + 64 * i;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int row = min(r0 + r, N - 1);  // rows past N repeat the last one; not written
+      wreg[r][i] = live && c < chunks ? reinterpret_cast<const uint4*>(W + (int64_t)row * K)[c]
+                                      : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  // the input vector: thread t builds chunks t and t + 256
+  uint32_t xv[2][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;
+    const uint4 v = c < chunks ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0u, 0u, 0u, 0u);
+    xv[i][0] = v.x;
+    xv[i][1] = v.y;
+    xv[i][2] = v.z;
+    xv[i][3] = v.w;
+    if (IN == 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ss += bf16_lo(xv[i][j]) * bf16_lo(xv[i][j]) + bf16_hi(xv[i][j]) * bf16_hi(xv[i][j]);
+    }
+  }
+  float inv = 1.0f;
+  if (IN == 1) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;
+    if (c < chunks) {
+      gemv_input<IN>(xv[i], aux, c, inv, per_dim);
+      xs[c] = make_uint4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) {
+      const uint4 v = xs[c];
+      const uint32_t xw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) acc[r] = dot8(wreg[r][i], xw, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float a = acc[r];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
+    if (lane == r && r0 + r < N) {
+      uint16_t o = f32_to_bf16(a);
+      if (res) o = f32_to_bf16(bf16_to_f32(res[r0 + r]) + bf16_to_f32(o));
+      y[r0 + r] = o;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace lq
+
+extern "C" int lq_gemv_fused(const uint16_t* W, const uint16_t* x, const uint16_t* aux,
+                             const uint16_t* res, uint16_t* y, int64_t N, int64_t K, int mode,
+                             float eps, int per_dim, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(N >= 1 && N <= (1 << 26) && K >= 8 && K <= 512 * MAXC && K % 8 == 0,
+               "bad fused GEMV shape N=%lld K=%lld (K a multiple of 8, at most %d)", (long long)N,
+               (long long)K, 512 * MAXC);
+  LQ_CHECK_ARG(mode == 1 || (mode == 2 && K % ND == 0), "mode must be 1 (RMSNorm input) or 2 "
+               "(gated attention input, K a multiple of 128)");
+  LQ_CHECK_ARG(W && x && aux && y, "null pointer");
+  LQ_CHECK_ARG(!res || res == y || (res + N <= y || y + N <= res), "res and y overlap partly");
+  hipStream_t st = (hipStream_t)stream;
+  const bool two = N >= 4 * 2 * 2 * device_cu_count();
+  const unsigned grid = (unsigned)(((two ? (N + 1) / 2 : N) + 3) / 4);
+  if (mode == 1) {
+    if (two)
+      gemv_fused_kernel<2, 1><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
+    else
+      gemv_fused_kernel<1, 1><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
+  } else {
+    if (two)
+      gemv_fused_kernel<2, 2><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
+    else
+      gemv_fused_kernel<1, 2><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
+  }
+  LQ_CHECK_LAUNCH("gemv_fused_kernel");
+  return LQ_OK;
+}
 
 extern "C" int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N,
                             int64_t K, void* stream) {

@@ -1,14 +1,13 @@
 """One decoded token through the attention blocks of a stack of full-attention layers, eager or as
 one HIP graph per token.
 
-Per layer (``laguna_mlx/laguna.py:94-111`` and the decoder layer around it): the residual add of
-the previous block's output fused with this layer's input RMSNorm (``lq_add_rms_norm``), then the
-attention block (:class:`lagunalab_amd.attention.Attention`: projection GEMM, ``lq_qk_norm_rope``,
-the fused decode step over the layer's 8-bit cache, ``lq_gate_heads``, ``o_proj`` GEMM). The MLP /
-MoE half of the layer is not part of this path.
+Per layer (``laguna_mlx/laguna.py:94-111`` and the decoder layer around it): the layer's input
+RMSNorm, the attention block of :class:`lagunalab_amd.attention.Attention` (projections,
+q/k RMSNorm + RoPE, the fused decode step over the layer's 8-bit cache, softplus gate, o_proj)
+and the residual add, in four launches (:class:`DecodeStack`). The MLP / MoE half of the layer is
+not part of this path.
 
-A decode step is ~7 launches per layer and the host (Python, ctypes) takes longer to issue them
-than the GPU to run them. :meth:`DecodeStack.capture` records the whole step once into a HIP graph
+The host (Python, ctypes) takes longer to issue a step's launches than the GPU to run them. :meth:`DecodeStack.capture` records the whole step once into a HIP graph
 (``torch.cuda.CUDAGraph``) whose launches read the token position from device memory: the RoPE
 offsets and the fused decode step's append row (``lq_q8_decode_append_attn_pos``) come from one
 int32 counter that the graph's last launch increments, so each replay decodes the next token. The
@@ -37,9 +36,25 @@ def add_rms_norm(h: torch.Tensor, d: torch.Tensor | None, w: torch.Tensor, eps: 
     return y
 
 
+def _gemv_fused(w, x, aux, res, y, mode, eps, per_dim=0):
+    lib = _lib.load()
+    dev = x.device
+    _lib.check(lib.lq_gemv_fused(w.data_ptr(), x.data_ptr(), aux.data_ptr(),
+                                 res.data_ptr() if res is not None else None, y.data_ptr(),
+                                 w.shape[0], w.shape[1], mode, float(eps), per_dim,
+                                 _lib.stream_ptr(dev)), "lq_gemv_fused")
+    return y
+
+
 class DecodeStack:
     """``blocks`` (:class:`Attention`), ``norms`` (input RMSNorm weights, bf16 [C]) and ``caches``
-    (``DequantKVCache(fused_decode=True)``, one sequence, equal offsets) of the layers in order."""
+    (``DequantKVCache(fused_decode=True)``, one sequence, equal offsets) of the layers in order.
+
+    A layer of a step is four launches: the input projection with the layer's input RMSNorm in
+    its prologue (``lq_gemv_fused`` mode 1), ``lq_qk_norm_rope``, the fused decode step, and the
+    output projection with the softplus gate in its prologue and the residual add in its epilogue
+    (mode 2). :meth:`step` issues them from the host; :meth:`capture` records them once into a
+    HIP graph that :meth:`replay` runs per token."""
 
     def __init__(self, blocks: list[Attention], norms: list[torch.Tensor],
                  caches: list[DequantKVCache], eps: float = 1e-6):
@@ -50,46 +65,55 @@ class DecodeStack:
                 raise ValueError("the layers need fused 8-bit caches")
         self.blocks, self.norms, self.caches, self.eps = blocks, norms, caches, eps
         self.graph = None
+        self.pos = None
 
-    def step(self, x: torch.Tensor) -> torch.Tensor:
-        """Eager decode of one token: ``x`` [1, 1, C] bf16, the residual stream in; returns it out."""
-        h, d = x.clone(), None
-        for blk, wn, c in zip(self.blocks, self.norms, self.caches):
-            y = add_rms_norm(h, d, wn, self.eps)
-            d = blk(y, None, c)
-        return h + d
-
-    # ---- graph path
-    def _block_pos(self, blk: Attention, y, cache, ws, n_plan):
+    def _layer(self, blk: Attention, wn, cache, h, ws=None, n_plan=None):
+        """One layer on the residual stream h [1, 1, C] (updated in place). Host mode (``ws`` None):
+        the cache reserves the row and the fused step gets its length from the host; graph mode:
+        positions from ``self.pos``, workspace ``ws`` and plan length ``n_plan``."""
+        from .q8_attn import decode_append_attention
         lib = _lib.load()
-        dev = y.device
+        dev = h.device
         sp = _lib.stream_ptr(dev)
         H, Hkv, D = blk.n_heads, blk.n_kv_heads, blk.head_dim
-        proj = linear(y, blk.w_in)  # [1, 1, (H + 2 Hkv) D + gate]
+        proj = torch.empty((1, 1, blk.w_in.shape[0]), dtype=torch.bfloat16, device=dev)
+        _gemv_fused(blk.w_in, h, wn, None, proj, 1, self.eps)
         q, k, v, g = torch.split(proj, blk._splits, dim=-1)  # contiguous pieces of one row
+        q4, k4, v4 = (t.view(1, hh, 1, D) for t, hh in ((q, H), (k, Hkv), (v, Hkv)))
+        host = ws is None
+        row = cache.q.reserve(k4, v4) if host else 0
         _lib.check(lib.lq_qk_norm_rope(q.data_ptr(), k.data_ptr(), q.data_ptr(), k.data_ptr(),
                                        blk.q_norm.data_ptr(), blk.k_norm.data_ptr(), 1, H, Hkv, 1,
                                        D, blk.eps, blk.inv_freq.data_ptr(), blk.rot_dims,
-                                       blk.mscale, 0, self.pos.data_ptr(), sp), "lq_qk_norm_rope")
-        (kc, ks, kb), (vc, vs, vb) = cache.q.keys, cache.q.values
-        cap = kc.shape[2]
-        out = torch.empty((1, H, 1, D), dtype=torch.bfloat16, device=dev)
-        _lib.check(lib.lq_q8_decode_append_attn_pos(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
-            vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, H, Hkv, D, cap, n_plan,
-            self.pos.data_ptr(), float(blk.scale), out.data_ptr(), ws.data_ptr(), ws.numel(), sp),
-            "lq_q8_decode_append_attn_pos")
-        gated = torch.empty((1, 1, H, D), dtype=torch.bfloat16, device=dev)
-        _lib.check(lib.lq_gate_heads(out.data_ptr(), g.data_ptr(), gated.data_ptr(), 1, H, 1, D,
-                                     0 if blk.per_head_gate else 1, sp), "lq_gate_heads")
-        return linear(gated.reshape(1, 1, H * D), blk.wo)
+                                       blk.mscale, int(row), None if host else self.pos.data_ptr(),
+                                       sp), "lq_qk_norm_rope")
+        if host:
+            out = decode_append_attention(q4, k4, v4, cache.q.keys, cache.q.values, n=row,
+                                          scale=blk.scale)
+        else:
+            (kc, ks, kb), (vc, vs, vb) = cache.q.keys, cache.q.values
+            out = torch.empty((1, H, 1, D), dtype=torch.bfloat16, device=dev)
+            _lib.check(lib.lq_q8_decode_append_attn_pos(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), ks.data_ptr(),
+                kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, H, Hkv, D,
+                kc.shape[2], n_plan, self.pos.data_ptr(), float(blk.scale), out.data_ptr(),
+                ws.data_ptr(), ws.numel(), sp), "lq_q8_decode_append_attn_pos")
+        _gemv_fused(blk.wo, out, g, h, h, 2, self.eps, 0 if blk.per_head_gate else 1)
 
+    def step(self, x: torch.Tensor) -> torch.Tensor:
+        """Eager decode of one token: ``x`` [1, 1, C] bf16, the residual stream in; returns it out."""
+        h = x.to(torch.bfloat16).clone()
+        for blk, wn, c in zip(self.blocks, self.norms, self.caches):
+            c._flush()
+            self._layer(blk, wn, c, h)
+        return h
+
+    # ---- graph path
     def _step_pos(self):
-        h, d = self.x_in.clone(), None
+        h = self.x_in.clone()
         for i, (blk, wn, c) in enumerate(zip(self.blocks, self.norms, self.caches)):
-            y = add_rms_norm(h, d, wn, self.eps)
-            d = self._block_pos(blk, y, c, self.ws[i], self.n_plan)
-        self.x_out.copy_(h + d)
+            self._layer(blk, wn, c, h, self.ws[i], self.n_plan)
+        self.x_out.copy_(h)
         self.pos.add_(1)  # the next replay decodes the next token
 
     def capture(self, steps: int):

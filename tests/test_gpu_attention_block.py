@@ -165,6 +165,41 @@ def test_gemv_matches_float64(dev, N, K):
     assert y.shape == (1, 1, N) and bool(((y.double() - want).abs() <= bound).all())
 
 
+@pytest.mark.parametrize("mode,per_dim", [(1, 0), (2, 0), (2, 1)])
+def test_gemv_fused_matches_restatement(dev, mode, per_dim):
+    """lq_gemv_fused: mode 1 = W (RMSNorm(h) w_norm), mode 2 = W (attn * softplus(gate)) plus the
+    residual, each against float64 products of the restatement's bf16 input vector (one fp32
+    accumulation and a bf16 rounding or two apart)."""
+    from lagunalab_amd import _lib
+    rng = np.random.default_rng(50 + mode + per_dim)
+    H, C = 8, 512
+    if mode == 1:
+        N, K = 3 * H * 128 + H, C
+        x, aux = _bf16(rng, (K,), 2.0), _bf16(rng, (K,), 0.1) + 1
+        xf = x.float()
+        xin = (xf * torch.rsqrt(xf.pow(2).mean() + 1e-6) * aux.float()).to(torch.bfloat16)
+        res = None
+    else:
+        N, K = C, H * 128
+        x = _bf16(rng, (K,))
+        aux = _bf16(rng, (K,) if per_dim else (H,), 3.0)
+        gate = torch.nn.functional.softplus(aux.float()).to(torch.bfloat16).float()
+        gate = gate if per_dim else gate.repeat_interleave(128)
+        xin = (x.float() * gate).to(torch.bfloat16)
+        res = _bf16(rng, (N,))
+    w = _bf16(rng, (N, K), 0.05)
+    y = torch.empty(N, dtype=torch.bfloat16, device=dev) if res is None else res.clone()
+    _lib.check(_lib.load().lq_gemv_fused(w.data_ptr(), x.data_ptr(), aux.data_ptr(),
+                                         y.data_ptr() if res is not None else None, y.data_ptr(),
+                                         N, K, mode, 1e-6, per_dim, _lib.stream_ptr(dev)), "fused")
+    want = w.double() @ xin.double()
+    mag = w.double().abs() @ xin.double().abs()
+    if res is not None:
+        want = want + res.double()
+        mag = mag + res.double().abs()
+    assert bool(((y.double() - want).abs() <= 2 * BF16_ULP * mag + 1e-4).all())
+
+
 def test_add_rms_norm_matches_restatement(dev):
     from lagunalab_amd.decoder import add_rms_norm
     rng = np.random.default_rng(21)
