@@ -251,6 +251,22 @@ int lq_gemv_fused(const uint16_t* W, const uint16_t* x, const uint16_t* aux, con
                   uint16_t* y, int64_t N, int64_t K, int mode, float eps, int per_dim,
                   void* stream);
 
+/*
+ * The input half of a decode step's attention block in one launch (one input row; laguna.py's
+ * input_layernorm, then laguna.py:97-101 at L = 1): y = W (RMSNorm(x) * norm_w) as lq_gemv_fused
+ * mode 1, then the first (Hq + Hkv) x 128 outputs, the q heads followed by the k heads, each get
+ * their RMSNorm (q_norm_w / k_norm_w, head_eps) and RoPE at position `offset` (or *offsets when
+ * offsets is non-null, a device int32) as lq_qk_norm_rope computes them, in place. N >= 128 (Hq +
+ * Hkv); the remaining outputs (v, gate logits) are plain projections. counters: Hq + Hkv uint32 in
+ * device memory, zero before the first call; every call leaves them zero. Calls that share
+ * counters must not overlap.
+ */
+int lq_gemv_norm_rope(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, uint16_t* y,
+                      int64_t N, int64_t K, float eps, const uint16_t* q_norm_w,
+                      const uint16_t* k_norm_w, int64_t Hq, int64_t Hkv, float head_eps,
+                      const float* inv_freq, int64_t rot_dims, float mscale, int64_t offset,
+                      const int32_t* offsets, uint32_t* counters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,45 @@ namespace {
 
 constexpr int ND = 128;  // head_dim
 
+// RMSNorm (times w, rounded to bf16) and RoPE at position `pos` of one head row held by one
+// wave: lane l holds dims 2l and 2l + 1 as the bf16 pair x2 (norm weights w2); returns the
+// lane's output pair.
+__device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,
+                                                   const float* __restrict__ inv_freq,
+                                                   int rot_dims, float mscale, float pos) {
+  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
+  float ss = x0 * x0 + x1 * x1;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const float inv = 1.0f / sqrtf(ss * (1.0f / ND) + eps);
+  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
+  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
+  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
+
+  const int half = rot_dims >> 1;      // rotated pairs
+  const int lane_off = rot_dims >> 2;  // partner lane distance
+  const bool rot = 2 * lane < rot_dims;
+  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
+  const float p0 = __shfl(y0, partner, 64);
+  const float p1 = __shfl(y1, partner, 64);
+  if (rot) {
+    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
+    const int i0 = first ? 2 * lane : 2 * lane - half;
+    float s0, c0, s1, c1;
+    sincosf(pos * inv_freq[i0], &s0, &c0);
+    sincosf(pos * inv_freq[i0 + 1], &s1, &c1);
+    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
+    if (first) {
+      y0 = a0 * c0 - b0 * s0;
+      y1 = a1 * c1 - b1 * s1;
+    } else {  // this lane holds x_{i+half}; the partner holds x_i
+      y0 = b0 * s0 + a0 * c0;
+      y1 = b1 * s1 + a1 * c1;
+    }
+  }
+  return (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+}
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_out, const uint16_t* __restrict__ q_w,
@@ -39,42 +78,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const uint16_t* in = (is_q ? q : k) + src_row * ND;
   uint16_t* out = (is_q ? q_out : k_out) + src_row * ND;
   const uint16_t* w = is_q ? q_w : k_w;
-
-  const uint32_t x2 = reinterpret_cast<const uint32_t*>(in)[lane];
-  const uint32_t w2 = reinterpret_cast<const uint32_t*>(w)[lane];
-  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
-  float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  const float inv = 1.0f / sqrtf(ss * (1.0f / ND) + eps);
-  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
-  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
-  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
-
-  const int half = rot_dims >> 1;      // rotated pairs
-  const int lane_off = rot_dims >> 2;  // partner lane distance
-  const bool rot = 2 * lane < rot_dims;
-  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
-  const float p0 = __shfl(y0, partner, 64);
-  const float p1 = __shfl(y1, partner, 64);
-  if (rot) {
-    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
-    const int i0 = first ? 2 * lane : 2 * lane - half;
-    const float pos = (float)((offsets ? (int64_t)offsets[b] : offset) + l);
-    float s0, c0, s1, c1;
-    sincosf(pos * inv_freq[i0], &s0, &c0);
-    sincosf(pos * inv_freq[i0 + 1], &s1, &c1);
-    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
-    if (first) {
-      y0 = a0 * c0 - b0 * s0;
-      y1 = a1 * c1 - b1 * s1;
-    } else {  // this lane holds x_{i+half}; the partner holds x_i
-      y0 = b0 * s0 + a0 * c0;
-      y1 = b1 * s1 + a1 * c1;
-    }
-  }
+  const float pos = (float)((offsets ? (int64_t)offsets[b] : offset) + l);
   reinterpret_cast<uint32_t*>(out)[lane] =
-      (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+      norm_rope_lane(reinterpret_cast<const uint32_t*>(in)[lane],
+                     reinterpret_cast<const uint32_t*>(w)[lane], lane, eps, inv_freq, rot_dims,
+                     mscale, pos);
 }
 
 // softplus(x) = log(1 + e^x), written as max(x, 0) + log1p(e^-|x|) (no overflow for large x)
@@ -216,39 +224,49 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restri
   }
 }
 
-// Input value chunk c of the fused GEMV (8 bf16 in four words), from the raw chunk xw.
-template <int IN>
-__device__ __forceinline__ void gemv_input(uint32_t (&xw)[4], const uint16_t* __restrict__ aux,
-                                           int c, float inv, int per_dim) {
-  if (IN == 1) {
-    const uint4 wn = reinterpret_cast<const uint4*>(aux)[c];
-    const uint32_t nw[4] = {wn.x, wn.y, wn.z, wn.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * inv * bf16_lo(nw[j])) |
-              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * inv * bf16_hi(nw[j])) << 16);
-  } else if (per_dim) {
-    const uint4 gv = reinterpret_cast<const uint4*>(aux)[c];
-    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float g0 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_lo(gw[j]))));
-      const float g1 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_hi(gw[j]))));
-      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * g0) |
-              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * g1) << 16);
-    }
-  } else {
-    const float gate = bf16_to_f32(f32_to_bf16(softplus_f(bf16_to_f32(aux[(8 * c) / ND]))));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xw[j] = (uint32_t)f32_to_bf16(bf16_lo(xw[j]) * gate) |
-              ((uint32_t)f32_to_bf16(bf16_hi(xw[j]) * gate) << 16);
-  }
+// The GEMVs of a decode step (one input row), with their neighbours fused in:
+//  * IN == 0: y = W x;
+//  * IN == 1 (input projection): x = RMSNorm(h) * w_in, the layer's input norm, each value
+//    rounded to bf16 as the separate norm would;
+//  * IN == 2 / 3 (output projection): x[k] = attn[k] * gate of k's head (IN 2: aux = gate logits
+//    [H]) or of k itself (IN 3: aux [K]), the gate softplus(logit) rounded to bf16, the product
+//    rounded to bf16 -- the gated attention output;
+//  * with `res`: y[n] = bf16(res[n] + bf16(W[n] . x)), the residual add (y may alias res).
+// Each thread first loads its two input chunks (thread t: chunks t and t + 256) and their aux
+// values, then every wave issues all its weight loads (RPW rows; lane l owns chunks l + 64 i,
+// i < NC), and while those are in flight the workgroup builds the input vector once into LDS
+// (the norm's sum of squares reduced over the workgroup); each wave then takes it from there.
+// No load sits under a branch: an index past the end is clamped to a valid address and its value
+// left unused (a branch around a load makes the compiler wait for every load in flight at the
+// join). NC > 0: K == 512 NC exactly; NC == 0: any K up to 512 MAXC, with run-time bounds.
+//
+// With EPI (input projection only, two rows per wave): the first `heads` x 128 outputs are the q
+// and k heads, and each head is normalized and rotated in place (norm_rope_lane) by the last of
+// its 16 workgroups to finish. Those workgroups store the head's rows with agent-scope stores
+// (written through to the device-coherent level), wait for them, then count their arrival on the
+// head's counter; the last arrival resets the counter to zero, and after an acquire fence its
+// first wave reads the head back and rewrites it.
+constexpr int MAXC = 8;
+struct HeadEpilogue {
+  const uint16_t* q_w;      // q_norm weights [128]
+  const uint16_t* k_w;      // k_norm weights [128]
+  const float* inv_freq;    // [rot_dims / 2]
+  const int32_t* offsets;   // device position (one sequence), or null: `offset`
+  uint32_t* counters;       // one per q/k head, zero between launches
+  int64_t offset;
+  int heads;                // Hq + Hkv
+  int q_heads;              // Hq
+  int rot_dims;
+  float eps, mscale;
+};
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
 // a + w . x over the 8 bf16 of one chunk
-__device__ __forceinline__ float dot8(const uint4 w, const uint32_t (&xw)[4], float a) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+__device__ __forceinline__ float dot8(const uint4 w, const uint4 x, float a) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xw[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     a = fmaf(bf16_lo(ww[j]), bf16_lo(xw[j]), a);
@@ -257,59 +275,63 @@ __device__ __forceinline__ float dot8(const uint4 w, const uint32_t (&xw)[4], fl
   return a;
 }
 
-// The two projections of a decode step with their neighbours fused in (one input row):
-//  * IN == 1 (input projection): x = RMSNorm(h) * w_in, the layer's input norm, each value
-//    rounded to bf16 as the separate norm would;
-//  * IN == 2 (output projection): x[k] = attn[k] * gate of k's head (softplus of the gate logit,
-//    rounded to bf16; per head or per dim), rounded to bf16 -- the gated attention output;
-//  * with `res`: y[n] = bf16(res[n] + bf16(W[n] . x)), the residual add (y may alias res).
-// Every wave first issues all its weight loads (lane l owns chunks l + 64 i, i < MAXC; K <= 512
-// MAXC), then the workgroup builds the input vector once into LDS (the norm's sum of squares
-// reduced over the workgroup), and each wave takes it from there.
-constexpr int MAXC = 8;
-template <int RPW, int IN>
-__global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* __restrict__ W,
-                                                         const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ aux,
+template <int RPW, int IN, bool EPI, int NC>
+__global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, const uint16_t* x,
+                                                         const uint16_t* aux,
                                                          const uint16_t* res, uint16_t* y, int N,
-                                                         int K, float eps, int per_dim) {
+                                                         int K, float eps, HeadEpilogue epi) {
+  static_assert(!EPI || (RPW == 2 && IN == 1), "the head epilogue runs on the input projection");
+  constexpr int NL = NC ? NC : MAXC;  // weight chunks per lane per row
   __shared__ uint4 xs[64 * MAXC];
   __shared__ float red[4];
+  __shared__ int sh_last;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int r0 = (blockIdx.x * 4 + (tid >> 6)) * RPW;
   const bool live = r0 < N;  // wave-uniform; every wave joins the barriers below
-  const int chunks = K >> 3;
-  uint4 wreg[RPW][MAXC];
+  const int chunks = NC ? 64 * NC : K >> 3;
+  const uint4* x4 = reinterpret_cast<const uint4*>(x);
+  const uint4* a4 = reinterpret_cast<const uint4*>(aux);
+
+  uint4 xin[2], ain[2];
+  uint16_t gin[2];
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
+  for (int i = 0; i < 2; ++i) {
+    const int cc = min(tid + 256 * i, chunks - 1);
+    xin[i] = x4[cc];
+    if (IN == 1 || IN == 3) ain[i] = a4[cc];
+    if (IN == 2) gin[i] = aux[(8 * cc) / ND];
+  }
+  // Keep the issue order: input loads, then weight loads, then the code that waits for the input
+  // (vmcnt counts in order, so the input is waited for with the weights still in flight). The
+  // pointers are not __restrict__, so no load moves across these memory barriers.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 wreg[RPW][NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int cc = min(lane + 64 * i, chunks - 1);
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       const int row = min(r0 + r, N - 1);  // rows past N repeat the last one; not written
-      wreg[r][i] = live && c < chunks ? reinterpret_cast<const uint4*>(W + (int64_t)row * K)[c]
-                                      : make_uint4(0u, 0u, 0u, 0u);
+      wreg[r][i] = reinterpret_cast<const uint4*>(W + (int64_t)row * K)[cc];
     }
   }
-  // the input vector: thread t builds chunks t and t + 256
-  uint32_t xv[2][4];
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + 256 * i;
-    const uint4 v = c < chunks ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0u, 0u, 0u, 0u);
-    xv[i][0] = v.x;
-    xv[i][1] = v.y;
-    xv[i][2] = v.z;
-    xv[i][3] = v.w;
-    if (IN == 1) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        ss += bf16_lo(xv[i][j]) * bf16_lo(xv[i][j]) + bf16_hi(xv[i][j]) * bf16_hi(xv[i][j]);
-    }
-  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
   float inv = 1.0f;
   if (IN == 1) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t xw[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        s += bf16_lo(xw[j]) * bf16_lo(xw[j]) + bf16_hi(xw[j]) * bf16_hi(xw[j]);
+      ss += tid + 256 * i < chunks ? s : 0.0f;
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if (lane == 0) red[tid >> 6] = ss;
@@ -318,38 +340,112 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* __restr
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int c = tid + 256 * i;
-    if (c < chunks) {
-      gemv_input<IN>(xv[i], aux, c, inv, per_dim);
-      xs[c] = make_uint4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+    const uint32_t xw[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
+    const uint32_t aw[4] = {ain[i].x, ain[i].y, ain[i].z, ain[i].w};
+    uint32_t ow[4];
+    if (IN == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ow[j] = xw[j];
+    } else if (IN == 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ow[j] = pack_bf16(bf16_lo(xw[j]) * inv * bf16_lo(aw[j]),
+                          bf16_hi(xw[j]) * inv * bf16_hi(aw[j]));
+    } else if (IN == 2) {
+      const float gate = bf16_to_f32(f32_to_bf16(softplus_f(bf16_to_f32(gin[i]))));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ow[j] = pack_bf16(bf16_lo(xw[j]) * gate, bf16_hi(xw[j]) * gate);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float g0 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_lo(aw[j]))));
+        const float g1 = bf16_to_f32(f32_to_bf16(softplus_f(bf16_hi(aw[j]))));
+        ow[j] = pack_bf16(bf16_lo(xw[j]) * g0, bf16_hi(xw[j]) * g1);
+      }
     }
+    const int c = tid + 256 * i;
+    if (c < chunks) xs[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
   }
   __syncthreads();
-  if (!live) return;
-  float acc[RPW];
+
+  const bool head_rows = EPI && blockIdx.x * 4 * RPW < 128 * epi.heads;  // workgroup-uniform
+  if (live) {
+    float acc[RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < chunks) {
-      const uint4 v = xs[c];
-      const uint32_t xw[4] = {v.x, v.y, v.z, v.w};
+    for (int i = 0; i < NL; ++i) {
+      const int c = lane + 64 * i;
+      const uint4 v = xs[min(c, chunks - 1)];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) acc[r] = dot8(wreg[r][i], xw, acc[r]);
+      for (int r = 0; r < RPW; ++r) {
+        const float a = dot8(wreg[r][i], v, acc[r]);
+        acc[r] = NC || c < chunks ? a : acc[r];
+      }
+    }
+    uint16_t o[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float a = acc[r];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
+      o[r] = f32_to_bf16(a);
+    }
+    if (head_rows) {  // rows r0, r0 + 1 of one q/k head (r0 even): one agent-scope word
+      if (lane == 0)
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(y + r0),
+                           (uint32_t)o[0] | ((uint32_t)o[RPW - 1] << 16), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        if (lane == r && r0 + r < N) {
+          uint16_t v = o[r];
+          if (res) v = f32_to_bf16(bf16_to_f32(res[r0 + r]) + bf16_to_f32(v));
+          y[r0 + r] = v;
+        }
+      }
     }
   }
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    float a = acc[r];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
-    if (lane == r && r0 + r < N) {
-      uint16_t o = f32_to_bf16(a);
-      if (res) o = f32_to_bf16(bf16_to_f32(res[r0 + r]) + bf16_to_f32(o));
-      y[r0 + r] = o;
-    }
+  if (!head_rows) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int head = (int)(blockIdx.x * 4 * RPW / 128);
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(epi.counters + head, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev + 1 == 128 / (4 * RPW);
+    if (last) __hip_atomic_store(epi.counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = last;
   }
+  __syncthreads();
+  if (!sh_last || tid >= 64) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  uint32_t* row = reinterpret_cast<uint32_t*>(y + (int64_t)head * 128);
+  const uint32_t x2 = __hip_atomic_load(row + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool is_q = head < epi.q_heads;
+  const uint32_t w2 = reinterpret_cast<const uint32_t*>(is_q ? epi.q_w : epi.k_w)[lane];
+  const float pos = (float)(epi.offsets ? (int64_t)epi.offsets[0] : epi.offset);
+  row[lane] = norm_rope_lane(x2, w2, lane, epi.eps, epi.inv_freq, epi.rot_dims, epi.mscale, pos);
+}
+
+// Launches gemv_fused_kernel for (N, K): two rows per wave once there are enough rows to fill the
+// chip with them (always with the head epilogue), exact-width variants for K = 2048 and 4096.
+template <int IN, bool EPI>
+void launch_gemv(const uint16_t* W, const uint16_t* x, const uint16_t* aux, const uint16_t* res,
+                 uint16_t* y, int64_t N, int64_t K, float eps, const HeadEpilogue& epi,
+                 hipStream_t st) {
+  const bool two = EPI || N >= 4 * 2 * 2 * device_cu_count();
+  const unsigned grid = (unsigned)(((two ? (N + 1) / 2 : N) + 3) / 4);
+#define LQ_GEMV(RPW, NC)                                                                    \
+  gemv_fused_kernel<RPW, IN, EPI, NC><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, \
+                                                           eps, epi)
+  if (two || EPI) {
+    if (K == 2048) LQ_GEMV(2, 4); else if (K == 4096) LQ_GEMV(2, 8); else LQ_GEMV(2, 0);
+  } else if constexpr (!EPI) {
+    if (K == 2048) LQ_GEMV(1, 4); else if (K == 4096) LQ_GEMV(1, 8); else LQ_GEMV(1, 0);
+  }
+#undef LQ_GEMV
 }
 
 }  // namespace
@@ -368,22 +464,43 @@ extern "C" int lq_gemv_fused(const uint16_t* W, const uint16_t* x, const uint16_
   LQ_CHECK_ARG(W && x && aux && y, "null pointer");
   LQ_CHECK_ARG(!res || res == y || (res + N <= y || y + N <= res), "res and y overlap partly");
   hipStream_t st = (hipStream_t)stream;
-  const bool two = N >= 4 * 2 * 2 * device_cu_count();
-  const unsigned grid = (unsigned)(((two ? (N + 1) / 2 : N) + 3) / 4);
-  if (mode == 1) {
-    if (two)
-      gemv_fused_kernel<2, 1><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
-    else
-      gemv_fused_kernel<1, 1><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
-  } else {
-    if (two)
-      gemv_fused_kernel<2, 2><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
-    else
-      gemv_fused_kernel<1, 2><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, eps, per_dim);
-  }
+  const HeadEpilogue none{};
+  if (mode == 1)
+    launch_gemv<1, false>(W, x, aux, res, y, N, K, eps, none, st);
+  else if (per_dim)
+    launch_gemv<3, false>(W, x, aux, res, y, N, K, eps, none, st);
+  else
+    launch_gemv<2, false>(W, x, aux, res, y, N, K, eps, none, st);
   LQ_CHECK_LAUNCH("gemv_fused_kernel");
   return LQ_OK;
 }
+
+extern "C" int lq_gemv_norm_rope(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w,
+                                 uint16_t* y, int64_t N, int64_t K, float eps,
+                                 const uint16_t* q_norm_w, const uint16_t* k_norm_w, int64_t Hq,
+                                 int64_t Hkv, float head_eps, const float* inv_freq,
+                                 int64_t rot_dims, float mscale, int64_t offset,
+                                 const int32_t* offsets, uint32_t* counters, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(K >= 8 && K <= 512 * MAXC && K % 8 == 0,
+               "bad input width K=%lld (a multiple of 8, at most %d)", (long long)K, 512 * MAXC);
+  LQ_CHECK_ARG(Hq >= 1 && Hkv >= 1 && Hq <= 1024 && Hkv <= 1024, "bad head counts");
+  LQ_CHECK_ARG(N >= ND * (Hq + Hkv) && N <= (1 << 26),
+               "N=%lld must hold the %lld q/k head rows", (long long)N,
+               (long long)(ND * (Hq + Hkv)));
+  LQ_CHECK_ARG(rot_dims >= 0 && rot_dims <= ND && rot_dims % 4 == 0,
+               "rot_dims must be a multiple of 4 in [0, 128] (got %lld)", (long long)rot_dims);
+  LQ_CHECK_ARG(offset >= 0, "negative offset");
+  LQ_CHECK_ARG(W && x && norm_w && y && q_norm_w && k_norm_w && counters &&
+               (inv_freq || rot_dims == 0), "null pointer");
+  HeadEpilogue epi{q_norm_w, k_norm_w, inv_freq, offsets, counters, offset, (int)(Hq + Hkv),
+                   (int)Hq, (int)rot_dims, head_eps, mscale};
+  launch_gemv<1, true>(W, x, norm_w, nullptr, y, N, K, eps, epi, (hipStream_t)stream);
+  LQ_CHECK_LAUNCH("gemv_fused_kernel");
+  return LQ_OK;
+}
+
 
 extern "C" int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N,
                             int64_t K, void* stream) {
@@ -393,6 +510,11 @@ extern "C" int lq_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, i
                "bad GEMV shape N=%lld K=%lld (K a multiple of 8)", (long long)N, (long long)K);
   LQ_CHECK_ARG(W && x && y, "null pointer");
   hipStream_t st = (hipStream_t)stream;
+  if (K <= 512 * MAXC) {  // the staged-input kernel
+    launch_gemv<0, false>(W, x, nullptr, nullptr, y, N, K, 0.0f, HeadEpilogue{}, st);
+    LQ_CHECK_LAUNCH("gemv_fused_kernel");
+    return LQ_OK;
+  }
   // two rows per wave once there are enough rows to fill the chip with them
   if (N >= 4 * 2 * 2 * device_cu_count()) {
     const int64_t waves = (N + 1) / 2;

@@ -4,12 +4,13 @@ one HIP graph per token.
 Per layer (``laguna_mlx/laguna.py:94-111`` and the decoder layer around it): the layer's input
 RMSNorm, the attention block of :class:`lagunalab_amd.attention.Attention` (projections,
 q/k RMSNorm + RoPE, the fused decode step over the layer's 8-bit cache, softplus gate, o_proj)
-and the residual add, in four launches (:class:`DecodeStack`). The MLP / MoE half of the layer is
+and the residual add, in three launches (:class:`DecodeStack`). The MLP / MoE half of the layer is
 not part of this path.
 
-The host (Python, ctypes) takes longer to issue a step's launches than the GPU to run them. :meth:`DecodeStack.capture` records the whole step once into a HIP graph
+The host (Python, ctypes) takes longer to issue a step's launches than the GPU to run them.
+:meth:`DecodeStack.capture` records the whole step once into a HIP graph
 (``torch.cuda.CUDAGraph``) whose launches read the token position from device memory: the RoPE
-offsets and the fused decode step's append row (``lq_q8_decode_append_attn_pos``) come from one
+position and the fused decode step's append row (``lq_q8_decode_append_attn_pos``) come from one
 int32 counter that the graph's last launch increments, so each replay decodes the next token. The
 caches' buffers are reserved for the replays beforehand (a replay never grows them) and their host
 offsets advance after each replay.
@@ -50,11 +51,12 @@ class DecodeStack:
     """``blocks`` (:class:`Attention`), ``norms`` (input RMSNorm weights, bf16 [C]) and ``caches``
     (``DequantKVCache(fused_decode=True)``, one sequence, equal offsets) of the layers in order.
 
-    A layer of a step is four launches: the input projection with the layer's input RMSNorm in
-    its prologue (``lq_gemv_fused`` mode 1), ``lq_qk_norm_rope``, the fused decode step, and the
-    output projection with the softplus gate in its prologue and the residual add in its epilogue
-    (mode 2). :meth:`step` issues them from the host; :meth:`capture` records them once into a
-    HIP graph that :meth:`replay` runs per token."""
+    A layer of a step is three launches: the input projection with the layer's input RMSNorm in
+    its prologue and the q/k RMSNorm + RoPE of each head in its epilogue (``lq_gemv_norm_rope``),
+    the fused decode step, and the output projection with the softplus gate in its prologue and
+    the residual add in its epilogue (``lq_gemv_fused`` mode 2). :meth:`step` issues them from
+    the host; :meth:`capture` records them once into a HIP graph that :meth:`replay` runs per
+    token."""
 
     def __init__(self, blocks: list[Attention], norms: list[torch.Tensor],
                  caches: list[DequantKVCache], eps: float = 1e-6):
@@ -66,6 +68,14 @@ class DecodeStack:
         self.blocks, self.norms, self.caches, self.eps = blocks, norms, caches, eps
         self.graph = None
         self.pos = None
+        self._cnt = None
+
+    def _counters(self, dev, n):
+        """Arrival counters of the input projection's head epilogue (zero between launches; the
+        launches of all layers share them, one after another on one stream)."""
+        if self._cnt is None or self._cnt.numel() < n:
+            self._cnt = torch.zeros(n, dtype=torch.int32, device=dev)
+        return self._cnt.data_ptr()
 
     def _layer(self, blk: Attention, wn, cache, h, ws=None, n_plan=None):
         """One layer on the residual stream h [1, 1, C] (updated in place). Host mode (``ws`` None):
@@ -77,16 +87,16 @@ class DecodeStack:
         sp = _lib.stream_ptr(dev)
         H, Hkv, D = blk.n_heads, blk.n_kv_heads, blk.head_dim
         proj = torch.empty((1, 1, blk.w_in.shape[0]), dtype=torch.bfloat16, device=dev)
-        _gemv_fused(blk.w_in, h, wn, None, proj, 1, self.eps)
         q, k, v, g = torch.split(proj, blk._splits, dim=-1)  # contiguous pieces of one row
         q4, k4, v4 = (t.view(1, hh, 1, D) for t, hh in ((q, H), (k, Hkv), (v, Hkv)))
         host = ws is None
         row = cache.q.reserve(k4, v4) if host else 0
-        _lib.check(lib.lq_qk_norm_rope(q.data_ptr(), k.data_ptr(), q.data_ptr(), k.data_ptr(),
-                                       blk.q_norm.data_ptr(), blk.k_norm.data_ptr(), 1, H, Hkv, 1,
-                                       D, blk.eps, blk.inv_freq.data_ptr(), blk.rot_dims,
-                                       blk.mscale, int(row), None if host else self.pos.data_ptr(),
-                                       sp), "lq_qk_norm_rope")
+        _lib.check(lib.lq_gemv_norm_rope(
+            blk.w_in.data_ptr(), h.data_ptr(), wn.data_ptr(), proj.data_ptr(), blk.w_in.shape[0],
+            blk.w_in.shape[1], float(self.eps), blk.q_norm.data_ptr(), blk.k_norm.data_ptr(), H,
+            Hkv, float(blk.eps), blk.inv_freq.data_ptr(), blk.rot_dims, float(blk.mscale),
+            int(row), None if host else self.pos.data_ptr(), self._counters(dev, H + Hkv),
+            sp), "lq_gemv_norm_rope")
         if host:
             out = decode_append_attention(q4, k4, v4, cache.q.keys, cache.q.values, n=row,
                                           scale=blk.scale)
@@ -143,6 +153,7 @@ class DecodeStack:
             if nb < 0:
                 raise ValueError(lib.lq_last_error().decode())
             self.ws.append(torch.zeros(nb, dtype=torch.uint8, device=dev))  # counters start at 0
+        self._counters(dev, max(b.n_heads + b.n_kv_heads for b in self.blocks))
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):

@@ -152,7 +152,8 @@ def test_attention_block_prefill_decode_verify(dev):
         assert err <= 2e-2 * scale, (L, err, scale)
 
 
-@pytest.mark.parametrize("N,K", [(6176, 2048), (2048, 4096), (5, 8), (1, 520), (4099, 64)])
+@pytest.mark.parametrize("N,K", [(6176, 2048), (2048, 4096), (4608, 4096), (5, 8), (1, 520),
+                                 (4099, 64), (300, 8200)])
 def test_gemv_matches_float64(dev, N, K):
     """lq_gemv_bf16 against float64 products of the same bf16 values: within the fp32
     accumulation error plus one bf16 rounding of the result."""
@@ -165,14 +166,16 @@ def test_gemv_matches_float64(dev, N, K):
     assert y.shape == (1, 1, N) and bool(((y.double() - want).abs() <= bound).all())
 
 
-@pytest.mark.parametrize("mode,per_dim", [(1, 0), (2, 0), (2, 1)])
-def test_gemv_fused_matches_restatement(dev, mode, per_dim):
+@pytest.mark.parametrize("mode,per_dim,H,C", [(1, 0, 8, 512), (1, 0, 32, 2048), (2, 0, 8, 512),
+                                              (2, 1, 8, 512), (2, 0, 32, 2048), (2, 1, 32, 4608),
+                                              (1, 0, 1, 40)])
+def test_gemv_fused_matches_restatement(dev, mode, per_dim, H, C):
     """lq_gemv_fused: mode 1 = W (RMSNorm(h) w_norm), mode 2 = W (attn * softplus(gate)) plus the
     residual, each against float64 products of the restatement's bf16 input vector (one fp32
-    accumulation and a bf16 rounding or two apart)."""
+    accumulation and a bf16 rounding or two apart). Widths 2048 and 4096 take the exact-width
+    kernels, the others the bounds-checked one; one and two rows per wave both occur."""
     from lagunalab_amd import _lib
-    rng = np.random.default_rng(50 + mode + per_dim)
-    H, C = 8, 512
+    rng = np.random.default_rng(50 + mode + per_dim + H + C)
     if mode == 1:
         N, K = 3 * H * 128 + H, C
         x, aux = _bf16(rng, (K,), 2.0), _bf16(rng, (K,), 0.1) + 1
@@ -198,6 +201,45 @@ def test_gemv_fused_matches_restatement(dev, mode, per_dim):
         want = want + res.double()
         mag = mag + res.double().abs()
     assert bool(((y.double() - want).abs() <= 2 * BF16_ULP * mag + 1e-4).all())
+
+
+@pytest.mark.parametrize("H,Hkv,C,rot,device_pos", [(32, 8, 2048, 64, False), (32, 8, 2048, 128, True),
+                                                    (4, 2, 520, 0, False)])
+def test_gemv_norm_rope_equals_two_launches(dev, H, Hkv, C, rot, device_pos):
+    """lq_gemv_norm_rope = lq_gemv_fused mode 1 followed by lq_qk_norm_rope on the q and k heads,
+    bit for bit (the same arithmetic in one launch); a second call with the same counters gives
+    the same result (the counters were left at zero)."""
+    from lagunalab_amd import _lib
+    from lagunalab_amd.attention import rope_frequencies
+    lib = _lib.load()
+    rng = np.random.default_rng(H + C + rot)
+    N = (H + 2 * Hkv) * 128 + H
+    w, x = _bf16(rng, (N, C), 0.05), _bf16(rng, (C,), 2.0)
+    wn, qn, kn = (_bf16(rng, (n,), 0.1) + 1 for n in (C, 128, 128))
+    params = {"rope_theta": 1e6, "partial_rotary_factor": rot / 128}
+    inv, rot_dims, mscale = rope_frequencies(128, params) if rot else (torch.ones(1), 0, 1.0)
+    inv = inv.to(dev)
+    pos = 81234
+    offs = torch.tensor([pos], dtype=torch.int32, device=dev) if device_pos else None
+    sp = _lib.stream_ptr(dev)
+    want = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.lq_gemv_fused(w.data_ptr(), x.data_ptr(), wn.data_ptr(), None, want.data_ptr(),
+                                 N, C, 1, 1e-6, 0, sp), "fused")
+    q, k = want[:H * 128], want[H * 128:(H + Hkv) * 128]
+    _lib.check(lib.lq_qk_norm_rope(q.data_ptr(), k.data_ptr(), q.data_ptr(), k.data_ptr(),
+                                   qn.data_ptr(), kn.data_ptr(), 1, H, Hkv, 1, 128, 1e-5,
+                                   inv.data_ptr(), rot_dims, mscale, pos, None, sp), "rope")
+    cnt = torch.zeros(H + Hkv, dtype=torch.int32, device=dev)
+    for _ in range(2):
+        y = torch.full((N,), 7.0, dtype=torch.bfloat16, device=dev)
+        _lib.check(lib.lq_gemv_norm_rope(
+            w.data_ptr(), x.data_ptr(), wn.data_ptr(), y.data_ptr(), N, C, 1e-6, qn.data_ptr(),
+            kn.data_ptr(), H, Hkv, 1e-5, inv.data_ptr(), rot_dims, mscale,
+            0 if device_pos else pos, offs.data_ptr() if device_pos else None, cnt.data_ptr(),
+            sp), "gemv_norm_rope")
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+        assert int(cnt.abs().sum()) == 0
 
 
 def test_add_rms_norm_matches_restatement(dev):
