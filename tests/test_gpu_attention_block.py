@@ -259,9 +259,15 @@ def test_add_rms_norm_matches_restatement(dev):
 
 
 def _stack(dev, seed, n0, layers=3, C=512, H=8, Hkv=2):
+    from lagunalab_amd.decoder import DecodeStack
+    return DecodeStack(*_layers(dev, seed, n0, layers, C, H, Hkv))
+
+
+def _layers(dev, seed, n0, layers=3, C=512, H=8, Hkv=2, fused=True):
+    """Blocks, input-norm weights and caches (n0 random prefill rows) of a layer stack; the same
+    seed gives the same weights and cache rows."""
     from lagunalab_amd.attention import Attention
     from lagunalab_amd.cache import DequantKVCache
-    from lagunalab_amd.decoder import DecodeStack
     rng = np.random.default_rng(seed)
     rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0, "partial_rotary_factor": 0.5,
             "original_max_position_embeddings": 4096}
@@ -272,10 +278,41 @@ def _stack(dev, seed, n0, layers=3, C=512, H=8, Hkv=2):
                                 w(H, C), _bf16(rng, (128,), 0.1) + 1, _bf16(rng, (128,), 0.1) + 1,
                                 H, Hkv, rope))
         norms.append(_bf16(rng, (C,), 0.1) + 1)
-        c = DequantKVCache(fused_decode=True)
+        c = DequantKVCache(fused_decode=fused)
         c.q.update_and_fetch(_bf16(rng, (1, Hkv, n0, 128)), _bf16(rng, (1, Hkv, n0, 128)))
         caches.append(c)
-    return DecodeStack(blocks, norms, caches)
+    return blocks, norms, caches
+
+
+@pytest.mark.parametrize("C,H,Hkv", [(512, 8, 2), (2048, 32, 8)])
+def test_stack_step_matches_restatement(dev, C, H, Hkv):
+    """DecodeStack.step (three fused launches per layer) against the float32 restatement of
+    each layer: h + o_proj(block(RMSNorm(h) w_norm)) with the reference's bf16 rounding points and
+    unfused attention over an unfused cache of the same rows; four tokens through three layers.
+    The gap allowed is the fused-vs-unfused attention difference carried through o_proj, plus a
+    bf16 rounding of the residual stream per layer."""
+    from lagunalab_amd.decoder import DecodeStack
+    stack = DecodeStack(*_layers(dev, 61, 4100, 3, C, H, Hkv))
+    blocks, norms, caches = _layers(dev, 61, 4100, 3, C, H, Hkv, fused=False)
+    rope = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0, "partial_rotary_factor": 0.5,
+            "original_max_position_embeddings": 4096}
+    refs = [RefBlock(b, rope) for b in blocks]
+    rng = np.random.default_rng(62)
+    for t in range(4):
+        x = _bf16(rng, (1, 1, C))
+        got = stack.step(x)
+        h = x.clone()
+        delta = 0.0
+        for ref, wn, c in zip(refs, norms, caches):
+            hf = h.float()
+            xn = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-6) * wn.float()).to(torch.bfloat16)
+            a = ref(xn, None, c)
+            delta = max(delta, float(a.float().abs().max()))
+            h = (h.float() + a.float()).to(torch.bfloat16)
+        err = (got.float() - h.float()).abs()
+        bound = 2e-2 * delta + 3 * BF16_ULP * h.float().abs()
+        assert bool((err <= bound).all()), (t, float(err.max()), delta)
+        assert all(c.offset == 4101 + t for c in stack.caches)
 
 
 def test_decode_pos_entry_matches_host_length(dev):
