@@ -55,13 +55,15 @@ def parse():
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "q4", "bf16", "ragged", "verify", "lookup", "layers"],
+                   choices=["decode", "q4", "bf16", "ragged", "verify", "lookup", "layers",
+                            "prefill"],
                    help="decode: the 8-bit decode step (default). q4 / bf16: decode attention over "
                         "a 4-bit / plain bf16 cache at the same context. ragged: 8 sequences of "
                         "default_rng(1) lengths in [42771, 82671]. verify: a 5-row causal verify "
                         "block over 65,536 cached rows plus its append. lookup: n-gram draft search "
                         "over 82,671 ids and greedy accept of 5 x 131,072 logits. layers: one decoded "
-                        "token through the attention blocks of --layers full-attention layers")
+                        "token through the attention blocks of --layers full-attention layers. "
+                        "prefill: a 2,048-row chunk appended and attended at --ctx rows")
     return p.parse_args()
 
 
@@ -326,6 +328,83 @@ def run_workload(args):
                 {"workload": f"ragged 8-bit decode attention, 8 sequences (sum {sum(lens)} tokens), "
                              f"{HQ}q/{HKV}kv heads, head_dim {D}, {nl} rotating caches",
                  "batch": B, "layers": nl}, extra)
+        return
+
+    if args.workload == "prefill":
+        # A 2,048-row prefill chunk at the end of an 82,671-row context: quantize-append of its
+        # K/V (rows 80,623 .. 82,670), then causal attention of its 32 x 2,048 query rows straight
+        # off the 8-bit cache (q8_prefill_attention: 16-position blocks through the verify
+        # kernel, no score matrix, no dequantized copy). 4 rotating layer caches.
+        from lagunalab_amd.q8_attn import q8_prefill_attention
+        n, L, nl = args.ctx, 2048, 4
+        nc = n - L
+        cap = (n + 255) // 256 * 256
+        layers = []
+        for _ in range(nl):
+            lay = []
+            for _kv in range(2):
+                x = torch.randn((1, HKV, nc, D), device=dev, generator=g).to(torch.bfloat16)
+                codes = torch.zeros((1, HKV, cap, D), dtype=torch.uint8, device=dev)
+                sc = torch.zeros((1, HKV, cap, 2), dtype=torch.bfloat16, device=dev)
+                bi = torch.zeros_like(sc)
+                _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, nc, D, codes.data_ptr(),
+                                                  sc.data_ptr(), bi.data_ptr(), cap, 0, 8, GS, sp),
+                           "prefill quantize")
+                del x
+                lay.append((codes, sc, bi))
+            layers.append(lay)
+        qv = torch.randn((1, HQ, L, D), device=dev, generator=g).to(torch.bfloat16)
+        kn = torch.randn((1, HKV, L, D), device=dev, generator=g).to(torch.bfloat16)
+        vn = torch.randn((1, HKV, L, D), device=dev, generator=g).to(torch.bfloat16)
+
+        def call(j):
+            (kc, ks, kb), (vc, vs, vb) = layers[j % nl]
+            _lib.check(lib.lq_quantize_append_kv(kn.data_ptr(), vn.data_ptr(), 1, HKV, L, D,
+                                                 kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                                 vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), cap,
+                                                 nc, 8, GS, sp), "chunk append")
+            q8_prefill_attention(qv, layers[j % nl][0], layers[j % nl][1], n, scale)
+        steps = max(1, min(args.steps, 32))
+        for j in range(min(args.warmup, 4)):
+            call(j)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for j in range(steps):
+            call(j)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        keys = L * nc + L * (L + 1) // 2  # keys seen, summed over the chunk's rows
+        flops = 4 * D * HQ * keys
+        tf = flops / (ms * 1e-3) / 1e12
+        extra = {"ms_per_chunk": round(ms, 3), "timed_chunks": steps,
+                 "rows_per_s": round(L / (ms * 1e-3), 1),
+                 "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "kernel": "lq_quantize_append_kv + 128 x (q8_attn_dense_kernel<4, "
+                                        "true, 64> + decode_merge_kernel) per chunk",
+                              "flops_per_chunk": flops}}
+        if do_cpu:
+            from oracle import attention as A
+            cv = lambda t: t.cpu().numpy() if t.dtype == torch.uint8 else t.cpu().view(torch.int16).numpy().view(np.uint16)
+            kh = tuple(cv(t) for t in layers[(steps - 1) % nl][0])
+            vh = tuple(cv(t) for t in layers[(steps - 1) % nl][1])
+            ns = 4  # the chunk's last rows: keys n-4 .. n-1 seen
+            qn = qv[:, :, L - ns:].float().cpu().numpy()
+            fn = lambda: A.unfused_attention(qn, kh, vh, n, scale, causal=True)
+            t, calls = _time_cpu(fn, args.cpu_seconds, min_calls=2)
+            fl = 4 * D * HQ * sum(n - ns + i + 1 for i in range(ns))
+            extra["cpu_baseline"] = {
+                "value": round(fl / t / 1e12, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"median of {calls} oracle calls (dequantize + causal fp64 SDPA) for the "
+                          f"chunk's last {ns} rows over {n} keys; CPU: {_cpu_model()}"}
+        args.steps, args.warmup = steps, min(args.warmup, 4)
+        _result(f"q8 prefill attention TFLOP/s, {L}-row chunk at {n} keys", round(tf, 2),
+                "TFLOP/s", True, ms, args, "u8",
+                {"workload": f"append a {L}-row chunk + its causal attention over {n} rows, "
+                             f"{HQ}q/{HKV}kv heads, head_dim {D}, 8-bit cache, {nl} rotating caches",
+                 "q_len": L, "ctx": n, "layers": nl}, extra)
         return
 
     if args.workload == "verify":

@@ -12,6 +12,9 @@ Drop-in for ``laguna_mlx/cache.py``:
   step only; ``fused_decode`` sets ``fused_step`` and ``attend`` runs the fused HIP kernel.
   Extension (``fused_verify``, default: follows ``fused_decode``): multi-token steps of up to 16
   rows -- the speculative verify block -- also take a fused kernel (causal, bottom-right).
+  Extension (``fused_prefill``, default off): longer steps -- prefill chunks -- are quantized
+  into the cache and attended straight off it (blocked causal kernel, no dequantized copy, no
+  score matrix).
 * :func:`make_quantized_cache` -- per-layer factory (``cache.py:147-157``);
   :func:`make_trimmable_cache` / :class:`TrimmableWindowCache` -- the plain bf16 caches of the
   speculative loop (``cache.py:7-63``).
@@ -172,13 +175,14 @@ class DequantKVCache:
     indexing the returned tuples) writes the rows first."""
 
     def __init__(self, group_size=64, bits=8, quantized_decode=False, fused_decode=False,
-                 fused_verify=None):
-        if fused_decode and (bits, group_size) != (8, 64):
+                 fused_verify=None, fused_prefill=False):
+        if (fused_decode or fused_prefill) and (bits, group_size) != (8, 64):
             raise ValueError("fused_decode needs 8-bit, group_size 64")
         self.q = QuantizedKVCache(group_size=group_size, bits=bits)
         self.quantized_decode = quantized_decode
         self.fused_decode = fused_decode
         self.fused_verify = fused_decode if fused_verify is None else fused_verify
+        self.fused_prefill = fused_prefill
         self._quantized_step = False
         self.fused_step = False
         self._pending = None  # (keys, values, row) of a fused step until attend() writes it
@@ -201,6 +205,10 @@ class DequantKVCache:
             qk, qv = self.q.views()
             return _PendingRows(qk, self), _PendingRows(qv, self)
         qk, qv = self.q.update_and_fetch(keys, values)
+        if self.fused_prefill and L > 16:  # a prefill chunk: attend() reads the packed cache
+            self.fused_step = True
+            self._quantized_step = False
+            return qk, qv
         self._quantized_step = self.quantized_decode and L == 1
         if self._quantized_step:
             return qk, qv
@@ -210,10 +218,11 @@ class DequantKVCache:
 
     def attend(self, queries, scale):
         """Attention straight off the packed cache: the fused decode kernel for one query row,
-        the fused causal verify kernel for a block of up to 16 rows; the step's pending new rows
-        are appended by the same call."""
+        the fused causal verify kernel for a block of up to 16 rows, the blocked causal kernel
+        for longer chunks; the step's pending new rows are appended by the same call."""
         from .q8_attn import (decode_append_attention, q8_decode_attention,
-                              q8_verify_append_attention, q8_verify_attention)
+                              q8_prefill_attention, q8_verify_append_attention,
+                              q8_verify_attention)
 
         L = queries.shape[2]
         if self._pending is not None and self._pending[0].shape[2] == L:
@@ -230,6 +239,8 @@ class DequantKVCache:
         self._flush()
         if L == 1:
             return q8_decode_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
+        if L > 16:
+            return q8_prefill_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
         return q8_verify_attention(queries, self.q.keys, self.q.values, self.q.offset, scale)
 
     @property
@@ -269,13 +280,15 @@ class DequantKVCache:
     @property
     def meta_state(self):
         return self.q.meta_state + tuple(
-            str(int(x)) for x in (self.quantized_decode, self.fused_decode, self.fused_verify))
+            str(int(x)) for x in (self.quantized_decode, self.fused_decode, self.fused_verify,
+                                  self.fused_prefill))
 
     @meta_state.setter
     def meta_state(self, v):
         self.q.meta_state = v[:4]
         self.quantized_decode, self.fused_decode, self.fused_verify = (bool(int(x)) for x in v[4:7])
-        if self.fused_decode and (self.q.bits, self.q.group_size) != (8, 64):
+        self.fused_prefill = len(v) > 7 and bool(int(v[7]))
+        if (self.fused_decode or self.fused_prefill) and (self.q.bits, self.q.group_size) != (8, 64):
             raise ValueError("fused_decode needs 8-bit, group_size 64")
 
     def is_trimmable(self):
@@ -478,11 +491,12 @@ def make_trimmable_cache(model, slack=64):
 
 
 def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, fused_decode=False,
-                         trim_slack=None):
+                         trim_slack=None, fused_prefill=False):
     """Quantized KV storage on full-attention layers; sliding layers keep their window
-    (``laguna_mlx/cache.py:147-157``). Extension: with ``trim_slack`` the sliding layers get
+    (``laguna_mlx/cache.py:147-157``). Extensions: with ``trim_slack`` the sliding layers get
     :class:`TrimmableWindowCache` with that slack, so that every layer can be trimmed and the
-    speculative loop can run over the quantized cache."""
+    speculative loop can run over the quantized cache; ``fused_prefill`` is passed to every
+    :class:`DequantKVCache`."""
     a = model.args
     if a.head_dim % group_size:
         raise ValueError(f"head_dim {a.head_dim} is not a multiple of group_size {group_size}")
@@ -495,6 +509,7 @@ def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, f
     return [
         window() if lt == "sliding_attention" else DequantKVCache(group_size=group_size, bits=bits,
                                                                   quantized_decode=quantized_decode,
-                                                                  fused_decode=fused_decode)
+                                                                  fused_decode=fused_decode,
+                                                                  fused_prefill=fused_prefill)
         for lt in a.layer_types
     ]

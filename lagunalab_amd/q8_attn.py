@@ -297,3 +297,61 @@ def q8_verify_append_attention(q, k_new, v_new, keys, values, n, scale):
                                       _lib.stream_ptr(dev))
     _lib.check(st, "lq_q8_verify_append_attn")
     return out.to(q.dtype)
+
+
+def q8_prefill_attention(q, keys, values, n, scale):
+    """Causal attention of a prefill chunk over the 8-bit cache, without materializing the score
+    matrix or a dequantized copy of the cache (the step before decode: ``L`` > 1 chunks on the
+    quantized cache, ``laguna_mlx/cache.py:99-100``, whose reference path dequantizes the whole
+    cache and runs SDPA; ``tests/test_cache.py:79-93`` guards its peak memory).
+
+    q [B, Hq, L, 128] for the chunk's positions n-L .. n-1, whose K/V are already the last L of
+    the first ``n`` cache rows; row i sees keys 0 .. n-L+i. Any L >= 1. The chunk runs as blocks
+    of P = min(16, 64 / G) positions through the verify kernel (one launch and one merge per
+    block; a ragged first block of L mod P rows), each block over the keys its last row sees.
+    Returns [B, Hq, L, 128] in q's dtype."""
+    lib = _lib.load()
+    B, Hq, L, D = q.shape
+    kc, ks, kb = keys
+    Hkv = kc.shape[1]
+    if D != 128 or Hkv < 1 or Hq % Hkv:
+        raise ValueError("prefill needs head_dim 128 and Hq a multiple of Hkv")
+    G = Hq // Hkv
+    if G > 64:
+        raise ValueError(f"{G} query heads per KV head exceed 64")
+    P = max(1, min(16, 64 // G))
+    if L <= P:
+        return q8_verify_attention(q, keys, values, n, scale)
+    n = int(n)
+    if not L <= n:
+        raise ValueError(f"n={n} must cover the {L} chunk rows")
+    r = L % P
+    out = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=q.device)
+    if r:
+        out[:, :, :r] = q8_verify_attention(q[:, :, :r].contiguous(), keys, values, n - L + r,
+                                            scale).to(torch.bfloat16)
+    nb = (L - r) // P
+    qb = q[:, :, r:].to(torch.bfloat16).reshape(B, Hq, nb, P, D).permute(2, 0, 1, 3, 4).contiguous()
+    # one validation pass through the checked wrapper (block 0), then the same call per block
+    ob = torch.empty_like(qb)
+    ob[0] = q8_verify_attention(qb[0], keys, values, n - L + r + P, scale).to(torch.bfloat16)
+    vc, vs, vb = values
+    kc8, vc8 = _as_bytes(kc), _as_bytes(vc)
+    ks, kb, vs, vb = (_bf16(t, "scales/biases") for t in (ks, kb, vs, vb))
+    cap = kc8.shape[2]
+    dev = q.device
+    ws_bytes = lib.lq_verify_workspace_bytes(B, Hq, Hkv, P, D, n)
+    if ws_bytes < 0:
+        raise ValueError(lib.lq_last_error().decode())
+    ws = _workspace(dev, ws_bytes)
+    sp = _lib.stream_ptr(dev)
+    blk = B * Hq * P * D * 2  # bytes per block of qb / ob
+    q0, o0 = qb.data_ptr(), ob.data_ptr()
+    for j in range(1, nb):
+        st = lib.lq_q8_verify_attn(q0 + j * blk, kc8.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                   vc8.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, P, D,
+                                   cap, n - L + r + P * (j + 1), float(scale), o0 + j * blk,
+                                   ws.data_ptr(), ws.numel(), sp)
+        _lib.check(st, "lq_q8_verify_attn")
+    out[:, :, r:] = ob.permute(1, 2, 0, 3, 4).reshape(B, Hq, L - r, D)
+    return out.to(q.dtype)

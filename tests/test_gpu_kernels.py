@@ -712,3 +712,70 @@ def test_fused_verify_step_in_cache(dev):
                   128 ** -0.5, causal=True)
     assert_attn_close(got, want.astype(np.float32), "fused verify vs dequantized",
                       REF_SMALL_N_ATOL, 0.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# prefill chunks straight off the 8-bit cache (no dequantized copy, no score matrix)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,L,G,Hkv", [(3000, 100, 4, 2), (700, 64, 8, 2), (33, 33, 1, 4),
+                                       (5000, 300, 4, 8), (2000, 17, 16, 1), (900, 40, 3, 2)])
+def test_prefill_matches_causal_oracle(dev, n, L, G, Hkv):
+    """q8_prefill_attention over n rows whose last L are the chunk's own: against the causal
+    fused-arithmetic and unfused oracles (blocks of min(16, 64 / G) positions, ragged first block
+    when L is not a multiple of it, a chunk that is the whole cache at n = L)."""
+    from lagunalab_amd.q8_attn import q8_prefill_attention
+    rng = np.random.default_rng(n + L + G)
+    cap = (n + 255) // 256 * 256
+    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (1, Hkv * G, L, 128))
+    got = q8_prefill_attention(to_dev_bf16(q, dev), kq, vq, n, 0.09)
+    assert got.shape == (1, Hkv * G, L, 128) and got.dtype == torch.bfloat16
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09, causal=True),
+                      f"fused prefill n={n} L={L} G={G}")
+    at, rt = unfused_tol(n)
+    assert_attn_close(got, A.unfused_attention(q, kn, vn, n, 0.09, causal=True),
+                      f"unfused prefill n={n} L={L} G={G}", at, rt)
+
+
+def test_prefill_blocks_equal_verify_calls(dev):
+    """Every block of a prefill chunk is the verify kernel's result for those rows, bit for bit
+    (16-row blocks at G = 4; rows 0..3 form the ragged first block)."""
+    from lagunalab_amd.q8_attn import q8_prefill_attention, q8_verify_attention
+    rng = np.random.default_rng(5)
+    n, L = 1500, 52
+    kq, vq = make_cache(rng, 1, 8, n, 1536, dev)
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, L, 128)), dev)
+    got = q8_prefill_attention(q, kq, vq, n, 0.09)
+    for a, b in ((0, 4), (4, 20), (20, 36), (36, 52)):
+        want = q8_verify_attention(q[:, :, a:b].contiguous(), kq, vq, n - L + b, 0.09)
+        assert torch.equal(got[:, :, a:b], want), (a, b)
+
+
+def test_prefill_never_materializes_scores(dev):
+    """A 2,048-row chunk over 10,240 rows (32q/8kv) allocates only the chunk-sized copies: the
+    score matrix alone would be 32 x 2,048 x 10,240 x 4 B = 2.7 GB (the reference's guard,
+    tests/test_cache.py:79-93: quantized prefill peak < plain + 100 MB)."""
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(6)
+    c = DequantKVCache(fused_decode=True, fused_prefill=True)
+    kv = lambda L: to_dev_bf16(Q.randn_bf16(rng, (1, 8, L, 128)), dev)
+    c.update_and_fetch(kv(8192), kv(8192))
+    q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, 2048, 128)), dev)
+    k, v = kv(2048), kv(2048)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    c.update_and_fetch(k, v)
+    assert c.fused_step
+    out = c.attend(q, 0.09)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    assert out.shape == (1, 32, 2048, 128)
+    assert peak < 100e6, peak
+    # rows 2040.. of the chunk against the oracle over the same cache
+    kn, vn = cache_np(c.q.keys), cache_np(c.q.values)
+    qs = q[:, :, 2040:].float().cpu().numpy()
+    want = A.fused_attention(qs, kn, vn, 10240, 0.09, causal=True)
+    assert_attn_close(out[:, :, 2040:], want, "prefill rows 2040..2047 at 10,240")

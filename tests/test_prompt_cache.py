@@ -34,7 +34,9 @@ def _layers(rng):
     tw = C.TrimmableWindowCache(window=8, slack=4)
     tw.state = (_bf16(rng, 12), _bf16(rng, 12))
     tw.meta_state = ("8", "4", "33")
-    return [q, q4, kv, rot, tw, C.DequantKVCache(), C.KVCache()]  # the last two empty
+    qp = C.DequantKVCache(fused_decode=True, fused_prefill=True)
+    qp.state = (_packed(rng, 40), _packed(rng, 40))
+    return [q, q4, kv, rot, tw, qp, C.DequantKVCache(), C.KVCache()]  # the last two empty
 
 
 def _same(a, b):
@@ -59,7 +61,8 @@ def test_round_trip_every_cache_class(tmp_path):
     assert not hasattr(got[0], "bits")  # the routing signal stays off after loading
     assert got[1].kv_bits == 4 and got[1].group_size == 64
     assert got[3].offset == 40 and got[4].offset == 33 and got[4].slack == 4
-    assert got[5].empty() and got[6].empty()
+    assert got[5].fused_prefill and got[5].offset == 40 and not got[0].fused_prefill
+    assert got[6].empty() and got[7].empty()
 
 
 def test_file_layout_follows_mlx_lm(tmp_path):
@@ -70,7 +73,7 @@ def test_file_layout_follows_mlx_lm(tmp_path):
     with safe_open(str(f), framework="pt") as h:
         keys, meta = set(h.keys()), h.metadata()
     assert {"0.0.0", "0.0.1", "0.0.2", "0.1.0", "0.1.1", "0.1.2", "2.0", "2.1"} <= keys
-    assert not any(k.startswith("5.") or k.startswith("6.") for k in keys)  # empty caches
+    assert "5.0.0" in keys and not any(k.startswith("6.") or k.startswith("7.") for k in keys)  # empty caches
     assert meta["2.0"] == "DequantKVCache" and meta["2.2"] == "KVCache"
     assert [meta[f"0.0.{j}"] for j in range(4)] == ["256", "300", "64", "8"]  # step, offset, g, bits
     assert meta["0.3.0"] == "8" and meta["0.3.1"] == "40"
@@ -89,6 +92,14 @@ def test_loaded_quantized_cache_keeps_growing(tmp_path):
                     torch.zeros(1, 2, 3, 128, dtype=torch.bfloat16))
     assert row == 300 and r.offset == 303 and r.keys[0].shape[2] == 300 + 256
     assert torch.equal(r.keys[0][:, :, :300], q.keys[0])
+
+
+def test_meta_state_without_the_prefill_switch_loads(tmp_path):
+    """A seven-entry meta_state (no fused_prefill entry) loads with fused_prefill off."""
+    c = C.DequantKVCache()
+    c.meta_state = ("256", "0", "64", "8", "0", "1", "1")
+    assert c.fused_decode and c.fused_verify and not c.fused_prefill
+    assert c.meta_state[-1] == "0" and len(c.meta_state) == 8
 
 
 def test_fused_meta_state_checks_the_format(tmp_path):
