@@ -333,8 +333,8 @@ def run_workload(args):
     if args.workload == "prefill":
         # A 2,048-row prefill chunk at the end of an 82,671-row context: quantize-append of its
         # K/V (rows 80,623 .. 82,670), then causal attention of its 32 x 2,048 query rows straight
-        # off the 8-bit cache (q8_prefill_attention: 16-position blocks through the verify
-        # kernel, no score matrix, no dequantized copy). 4 rotating layer caches.
+        # off the 8-bit cache (q8_prefill_attention -> lq_q8_prefill_attn: no score matrix, no
+        # dequantized copy). 4 rotating layer caches.
         from lagunalab_amd.q8_attn import q8_prefill_attention
         n, L, nl = args.ctx, 2048, 4
         nc = n - L
@@ -382,8 +382,8 @@ def run_workload(args):
                  "rows_per_s": round(L / (ms * 1e-3), 1),
                  "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0,
                               "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
-                              "kernel": "lq_quantize_append_kv + 128 x (q8_attn_dense_kernel<4, "
-                                        "true, 64> + decode_merge_kernel) per chunk",
+                              "kernel": "lq_quantize_append_kv + q8_prefill_kernel "
+                                        "(lq_q8_prefill_attn) per chunk",
                               "flops_per_chunk": flops}}
         if do_cpu:
             from oracle import attention as A

@@ -252,6 +252,22 @@ int lq_gemv_fused(const uint16_t* W, const uint16_t* x, const uint16_t* aux, con
                   void* stream);
 
 /*
+ * Causal attention of a prefill chunk over the 8-bit cache, without the score matrix or a
+ * dequantized copy of the cache (replaces, for prefill chunks, DequantKVCache's dequantize,
+ * laguna_mlx/cache.py:99-100, and the SDPA of laguna.py:107 with the causal mask; the reference
+ * guards the peak memory of that path in tests/test_cache.py:79-93):
+ *   q   bf16 [B, Hq, L, D] contiguous, D == 128, Hq / Hkv in {1, 2, 4, 8}; the chunk's positions
+ *       are n-L .. n-1, their K/V already the last L of the first n cache rows; row i sees keys
+ *       0 .. n-L+i.
+ *   out bf16 [B, Hq, L, D]
+ * No workspace.
+ */
+int lq_q8_prefill_attn(const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint16_t* kb,
+                       const uint8_t* vc, const uint16_t* vs, const uint16_t* vb, int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t L, int64_t D, int64_t cap, int64_t n,
+                       float scale, uint16_t* out, void* stream);
+
+/*
  * The input half of a decode step's attention block in one launch (one input row; laguna.py's
  * input_layernorm, then laguna.py:97-101 at L = 1): y = W (RMSNorm(x) * norm_w) as lq_gemv_fused
  * mode 1, then the first (Hq + Hkv) x 128 outputs, the q heads followed by the k heads, each get

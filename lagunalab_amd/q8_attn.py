@@ -306,16 +306,52 @@ def q8_prefill_attention(q, keys, values, n, scale):
     cache and runs SDPA; ``tests/test_cache.py:79-93`` guards its peak memory).
 
     q [B, Hq, L, 128] for the chunk's positions n-L .. n-1, whose K/V are already the last L of
-    the first ``n`` cache rows; row i sees keys 0 .. n-L+i. Any L >= 1. The chunk runs as blocks
-    of P = min(16, 64 / G) positions through the verify kernel (one launch and one merge per
-    block; a ragged first block of L mod P rows), each block over the keys its last row sees.
-    Returns [B, Hq, L, 128] in q's dtype."""
-    lib = _lib.load()
+    the first ``n`` cache rows; row i sees keys 0 .. n-L+i. Any L >= 1. Chunks of more than 16
+    rows with 1, 2, 4 or 8 query heads per KV head run ``lq_q8_prefill_attn`` (one launch: 256
+    query rows per workgroup over shared, once-dequantized K/V tiles); other shapes go through
+    the verify kernel block by block. Returns [B, Hq, L, 128] in q's dtype."""
     B, Hq, L, D = q.shape
     kc, ks, kb = keys
     Hkv = kc.shape[1]
     if D != 128 or Hkv < 1 or Hq % Hkv:
         raise ValueError("prefill needs head_dim 128 and Hq a multiple of Hkv")
+    if L <= 16:
+        return q8_verify_attention(q, keys, values, n, scale)
+    if Hq // Hkv not in (1, 2, 4, 8):
+        return _prefill_blocked(q, keys, values, n, scale)
+    lib = _lib.load()
+    vc, vs, vb = values
+    dev = _lib.require_device(q, kc, ks, kb, vc, vs, vb)
+    qb = _bf16(q.to(torch.bfloat16), "q")
+    kc, vc = _as_bytes(kc), _as_bytes(vc)
+    if kc.shape[-1] != D:
+        raise ValueError("prefill runs on the 8-bit cache only")
+    ks, kb, vs, vb = (_bf16(t, "scales/biases") for t in (ks, kb, vs, vb))
+    cap = kc.shape[2]
+    for t in (kc, vc):
+        if tuple(t.shape) != (B, Hkv, cap, D):
+            raise ValueError(f"cache buffer {tuple(t.shape)} does not match {(B, Hkv, cap, D)}")
+    for t in (ks, kb, vs, vb):
+        if tuple(t.shape) != (B, Hkv, cap, D // 64):
+            raise ValueError(f"scales/biases {tuple(t.shape)} do not match {(B, Hkv, cap, D // 64)}")
+    if not L <= int(n) <= cap:
+        raise ValueError(f"n={n} must cover the {L} chunk rows and fit the capacity {cap}")
+    out = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=dev)
+    st = lib.lq_q8_prefill_attn(qb.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, L, D, cap,
+                                int(n), float(scale), out.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(st, "lq_q8_prefill_attn")
+    return out.to(q.dtype)
+
+
+def _prefill_blocked(q, keys, values, n, scale):
+    """q8_prefill_attention for any head grouping: blocks of P = min(16, 64 / G) positions through
+    the verify kernel (one launch and one merge per block; a ragged first block of L mod P rows),
+    each block over the keys its last row sees."""
+    lib = _lib.load()
+    B, Hq, L, D = q.shape
+    kc, ks, kb = keys
+    Hkv = kc.shape[1]
     G = Hq // Hkv
     if G > 64:
         raise ValueError(f"{G} query heads per KV head exceed 64")

@@ -718,19 +718,22 @@ def test_fused_verify_step_in_cache(dev):
 # prefill chunks straight off the 8-bit cache (no dequantized copy, no score matrix)
 # ---------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n,L,G,Hkv", [(3000, 100, 4, 2), (700, 64, 8, 2), (33, 33, 1, 4),
-                                       (5000, 300, 4, 8), (2000, 17, 16, 1), (900, 40, 3, 2)])
-def test_prefill_matches_causal_oracle(dev, n, L, G, Hkv):
+@pytest.mark.parametrize("n,L,G,Hkv,B", [(3000, 100, 4, 2, 1), (700, 64, 8, 2, 1), (33, 33, 1, 4, 1),
+                                         (5000, 300, 4, 8, 1), (1200, 260, 2, 2, 2),
+                                         (513, 513, 4, 1, 1), (4200, 17, 8, 8, 1),
+                                         (2000, 17, 16, 1, 1), (900, 40, 3, 2, 1)])
+def test_prefill_matches_causal_oracle(dev, n, L, G, Hkv, B):
     """q8_prefill_attention over n rows whose last L are the chunk's own: against the causal
-    fused-arithmetic and unfused oracles (blocks of min(16, 64 / G) positions, ragged first block
-    when L is not a multiple of it, a chunk that is the whole cache at n = L)."""
+    fused-arithmetic and unfused oracles. G in {1, 2, 4, 8}: the prefill kernel (blocks of
+    256 / G positions, ragged last block, two sequences, a chunk that is the whole cache at
+    n = L so that most tiles are masked or skipped); G = 16 and 3: the blocked verify path."""
     from lagunalab_amd.q8_attn import q8_prefill_attention
-    rng = np.random.default_rng(n + L + G)
+    rng = np.random.default_rng(n + L + G + B)
     cap = (n + 255) // 256 * 256
-    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
-    q = Q.randn_bf16(rng, (1, Hkv * G, L, 128))
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (B, Hkv * G, L, 128))
     got = q8_prefill_attention(to_dev_bf16(q, dev), kq, vq, n, 0.09)
-    assert got.shape == (1, Hkv * G, L, 128) and got.dtype == torch.bfloat16
+    assert got.shape == (B, Hkv * G, L, 128) and got.dtype == torch.bfloat16
     kn, vn = cache_np(kq), cache_np(vq)
     assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09, causal=True),
                       f"fused prefill n={n} L={L} G={G}")
@@ -740,17 +743,20 @@ def test_prefill_matches_causal_oracle(dev, n, L, G, Hkv):
 
 
 def test_prefill_blocks_equal_verify_calls(dev):
-    """Every block of a prefill chunk is the verify kernel's result for those rows, bit for bit
-    (16-row blocks at G = 4; rows 0..3 form the ragged first block)."""
-    from lagunalab_amd.q8_attn import q8_prefill_attention, q8_verify_attention
+    """The blocked path: every block of a chunk is the verify kernel's result for those rows, bit
+    for bit (16-row blocks at G = 4; rows 0..3 form the ragged first block); and the prefill
+    kernel agrees with it within the attention tolerance."""
+    from lagunalab_amd.q8_attn import _prefill_blocked, q8_prefill_attention, q8_verify_attention
     rng = np.random.default_rng(5)
     n, L = 1500, 52
     kq, vq = make_cache(rng, 1, 8, n, 1536, dev)
     q = to_dev_bf16(Q.randn_bf16(rng, (1, 32, L, 128)), dev)
-    got = q8_prefill_attention(q, kq, vq, n, 0.09)
+    got = _prefill_blocked(q, kq, vq, n, 0.09)
     for a, b in ((0, 4), (4, 20), (20, 36), (36, 52)):
         want = q8_verify_attention(q[:, :, a:b].contiguous(), kq, vq, n - L + b, 0.09)
         assert torch.equal(got[:, :, a:b], want), (a, b)
+    assert_attn_close(q8_prefill_attention(q, kq, vq, n, 0.09), got.float().cpu().numpy(),
+                      "prefill kernel vs blocked path")
 
 
 def test_prefill_never_materializes_scores(dev):
