@@ -196,32 +196,37 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     if (t0 > lim_hi) continue;  // wave-uniform: no key of this tile is visible to its rows
     const bool full = t0 + PT - 1 <= lim_lo;
 
-    // Q.K^T: c[mt][nt] -- keys 16 mt + 4 lq4 + r of row 16 nt + lc (log2 units)
-    f4_t c[4][2];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int key = 16 * mt + lc;
-      const uint4* kr = reinterpret_cast<const uint4*>(sm.k + key * D);
-      c[mt][0] = c[mt][1] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint4 a = kr[(4 * kk + lq4) ^ lc];
-        const half8_t ah = words_as_h8(a.x, a.y, a.z, a.w);
-        c[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qb[0][kk], c[mt][0], 0, 0, 0);
-        c[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qb[1][kk], c[mt][1], 0, 0, 0);
-      }
-    }
-    uint32_t pw[2][2][4];  // P.V B operands [nt][k-step][dword]
+    // Per N tile: Q.K^T, softmax, P.V. The N tiles' chains are independent, so the second
+    // tile's MFMAs can run while the first tile's softmax (VALU, exp) issues.
+    // c: keys 16 mt + 4 lq4 + r of row 16 nt + lc (log2 units)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      float s[4][4];
+      f4_t c[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt) {
+        const int key = 16 * mt + lc;
+        const uint4* kr = reinterpret_cast<const uint4*>(sm.k + key * D);
+        c[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = c[mt][nt][r];
-          s[mt][r] = full || t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? v : -INFINITY;
+        for (int kk = 0; kk < 4; ++kk) {
+          const uint4 a = kr[(4 * kk + lq4) ^ lc];
+          c[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(words_as_h8(a.x, a.y, a.z, a.w),
+                                                         qb[nt][kk], c[mt], 0, 0, 0);
         }
+      }
+      float s[4][4];
+      if (full) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[mt][r] = c[mt][r];
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            s[mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? c[mt][r] : -INFINITY;
+      }
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -240,6 +245,7 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
       }
       const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float ls = 0.0f;
+      uint32_t pw[2][4];  // P.V B operands [k-step][dword]
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         float p[8];
@@ -251,23 +257,21 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
             ls += p[4 * hh + r];
           }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pw[nt][e][j] = pack_h2(p[2 * j], p[2 * j + 1]);
+        for (int j = 0; j < 4; ++j) pw[e][j] = pack_h2(p[2 * j], p[2 * j + 1]);
       }
       lsum[nt] += ls;
-    }
-    // P.V: out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
+      // P.V: out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < 2; ++e) {
+        const half8_t pb = words_as_h8(pw[e][0], pw[e][1], pw[e][2], pw[e][3]);
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = 16 * dt + lc;
-        const uint4 a = reinterpret_cast<const uint4*>(sm.vt + d * PT)[(4 * e + lq4) ^ ((d >> 1) & 7)];
-        const half8_t ah = words_as_h8(a.x, a.y, a.z, a.w);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              ah, words_as_h8(pw[nt][e][0], pw[nt][e][1], pw[nt][e][2], pw[nt][e][3]),
-              oacc[nt][dt], 0, 0, 0);
+        for (int dt = 0; dt < 8; ++dt) {
+          const int d = 16 * dt + lc;
+          const uint4 a =
+              reinterpret_cast<const uint4*>(sm.vt + d * PT)[(4 * e + lq4) ^ ((d >> 1) & 7)];
+          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(words_as_h8(a.x, a.y, a.z, a.w),
+                                                                pb, oacc[nt][dt], 0, 0, 0);
+        }
       }
     }
   }
