@@ -54,6 +54,24 @@ def test_model_decode_matches_dequant_cache(model):
 
 
 @torch.no_grad()
+def test_model_prefill_off_the_cache_matches_dequant_cache(model):
+    """A 300-token prompt prefilled in chunks of 200 and 100 through the prefill kernel
+    (``fused_prefill``: attention straight off the 8-bit cache) gives the logits of the
+    dequantize-then-SDPA cache within bf16 noise and the same argmax, and the decode steps after
+    it agree as well."""
+    ids = torch.tensor([[5, 9, 2, 7, 1, 3, 8, 4] * 40], device="cuda")[:, :300]
+    out = []
+    for fp in (False, True):
+        cache = make_quantized_cache(model, 8, fused_decode=fp, fused_prefill=fp)
+        logits = [model(ids[:, :200], cache=cache), model(ids[:, 200:], cache=cache)]
+        tok = torch.tensor([[6]], device="cuda")
+        logits += [model(tok, cache=cache) for _ in range(3)]
+        out.append(torch.cat(logits, dim=1))
+    assert (out[0] - out[1]).abs().max().item() < 5e-2 * out[0].abs().max().item()
+    assert torch.equal(out[0].argmax(-1), out[1].argmax(-1))
+
+
+@torch.no_grad()
 def test_fused_greedy_tokens_equal_unfused(model):
     want = _greedy(model, PROMPT, 40, _quantized(model, False))
     got = _greedy(model, PROMPT, 40, _quantized(model, True))
