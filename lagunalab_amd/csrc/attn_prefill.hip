@@ -8,12 +8,12 @@
 // Work: one workgroup of 8 waves per (sequence, KV head, block of 256 query rows), the rows
 // being PB = 256 / G positions of all G query heads of the KV head; wave w takes 32 rows (two
 // MFMA N tiles of 16) of one head. The workgroup walks the 64-key tiles up to its last row's
-// causal bound, and each tile is brought into LDS once for all 8 waves:
+// causal bound (128-key tiles), and each tile is brought into LDS once for all 8 waves:
 //  * the raw tile (K and V codes, 128 B per key each, and the four bf16 word arrays) is copied
-//    global -> LDS by DMA two tiles ahead (three raw slots, 3 copies per thread per tile, so a
-//    fixed vmcnt(3) finds tile t landed);
-//  * the workgroup dequantizes it once (scale * code + bias in fp32, rounded to fp16) into K [64
-//    keys][128 dims] and V^T [128 dims][64 keys], both XOR-swizzled by 16-byte chunk so that the
+//    global -> LDS by DMA one tile ahead (two raw slots, 5 copies per thread per tile), landing
+//    while the current tile is dequantized and computed;
+//  * the workgroup dequantizes it once (scale * code + bias in fp32, rounded to fp16) into K [128
+//    keys][128 dims] and V^T [128 dims][128 keys], both XOR-swizzled by 16-byte chunk so that the
 //    MFMA operand reads are conflict-free;
 //  * each wave then runs Q.K^T (v_mfma_f32_16x16x32_f16: M = 16 keys, N = 16 rows, K = 32 dims;
 //    q pre-scaled by scale * log2(e) in fp16), the online softmax with lazy rescaling (a lane
@@ -32,19 +32,20 @@ using namespace attn;
 
 constexpr int PW = 8;       // waves per workgroup
 constexpr int PROWS = 256;  // query rows per workgroup
-constexpr int PT = 64;      // keys per tile
+constexpr int PT = 128;     // keys per tile
+constexpr int PMT = PT / 16;  // M tiles (16 keys) per tile
+constexpr int PE = PT / 32;   // P.V k-steps (32 keys) per tile
 
 struct PrefillRaw {
   alignas(16) uint8_t k[PT * D];  // row-major [key][128 B]
   uint8_t v[PT * D];
-  uint32_t w[4][PT];      // K scale, K bias, V scale, V bias words (two bf16 groups each)
-  uint32_t dummy[4][PT];  // the copies of waves 4..7 (same words, never read)
+  uint32_t w[4][PT];              // K scale, K bias, V scale, V bias words (two bf16 groups each)
 };
 
 struct PrefillSmem {
-  PrefillRaw raw[3];
+  PrefillRaw raw[2];
   alignas(16) _Float16 k[PT * D];   // [key][dim], 16-byte chunk j of key r at chunk j ^ (r & 15)
-  alignas(16) _Float16 vt[D * PT];  // [dim][slot], 16-byte chunk j of dim d at j ^ ((d >> 1) & 7)
+  alignas(16) _Float16 vt[D * PT];  // [dim][slot], 16-byte chunk j of dim d at chunk j ^ (d & 15)
 };
 
 __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   // this wave's rows: head gh, positions p0 .. p0 + 31 (row 16 nt + lc of the wave: p0 + 16 nt + lc)
   const int gh = (32 * wv) / PB;
   const int p0 = pb * PB + (32 * wv) % PB;
-  const int lim_lo = base + p0;                      // bound of the wave's first row
+  const int lim_lo = base + p0;                                  // bound of the wave's first row
   const int lim_hi = p0 < L ? base + min(p0 + 31, L - 1) : -1;  // of its last valid row
   const int wg_last = min(pb * PB + PB - 1, L - 1);  // the workgroup's last valid position
   const int T = (base + wg_last) / PT + 1;           // tiles the workgroup needs
@@ -78,37 +79,40 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
   const int last_row = n - 1;
 
-  // ---- raw tile copies: K (1 KB per wave: keys 8 wv .. 8 wv + 7), V likewise, one word array
-  // per wave (waves 4..7 copy again into the dummy area)
+  // ---- raw tile copies, per thread: two 16-byte K copies (wave wv: keys 16 wv .. 16 wv + 15),
+  // two V copies, one word (wave wv: word array wv / 2, keys 64 (wv % 2) + lane)
   const uint32_t lds_raw = lds_addr(&sm.raw[0]);
-  const int ck = 8 * wv + (lane >> 3);  // key of this lane's 16-byte K / V copy
+  const int ck = 16 * wv + (lane >> 3);  // key of this lane's first K / V copy (second: + 8)
   const uint32_t cofs = 16u * (uint32_t)(lane & 7);
-  const uint16_t* warr = (wv & 3) == 0 ? ks : (wv & 3) == 1 ? kb : (wv & 3) == 2 ? vs : vb;
-  const uint32_t wdst = (wv < 4 ? offsetof(PrefillRaw, w) : offsetof(PrefillRaw, dummy)) +
-                        (uint32_t)(wv & 3) * PT * 4;
+  const int wa = wv >> 1;
+  const uint16_t* warr = wa == 0 ? ks : wa == 1 ? kb : wa == 2 ? vs : vb;
+  const int wkey = 64 * (wv & 1) + lane;
   auto issue = [&](int t, int slot) {
     const int t0 = PT * min(t, T - 1);
     const uint32_t lb = lds_raw + (uint32_t)slot * (uint32_t)sizeof(PrefillRaw);
     // M0 operands: wave-uniform values, made explicit so that they live in SGPRs
-    const uint32_t mk = __builtin_amdgcn_readfirstlane(lb + offsetof(PrefillRaw, k) + 1024u * wv);
-    const uint32_t mv = __builtin_amdgcn_readfirstlane(lb + offsetof(PrefillRaw, v) + 1024u * wv);
-    const uint32_t mw = __builtin_amdgcn_readfirstlane(lb + wdst);
-    const int64_t kr = row0 + min(t0 + ck, last_row);
-    const int64_t wr = row0 + min(t0 + lane, last_row);
+    const uint32_t mk = __builtin_amdgcn_readfirstlane(lb + offsetof(PrefillRaw, k) + 2048u * wv);
+    const uint32_t mv = __builtin_amdgcn_readfirstlane(lb + offsetof(PrefillRaw, v) + 2048u * wv);
+    const uint32_t mw = __builtin_amdgcn_readfirstlane(
+        lb + offsetof(PrefillRaw, w) + 4u * (uint32_t)(PT * wa + 64 * (wv & 1)));
+    const int64_t kr0 = row0 + min(t0 + ck, last_row);
+    const int64_t kr1 = row0 + min(t0 + ck + 8, last_row);
+    const int64_t wr = row0 + min(t0 + wkey, last_row);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :: "v"(kc + kr * D + cofs), "s"(mk)
-                 : "memory");
+                 :: "v"(kc + kr0 * D + cofs), "s"(mk) : "memory");
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :: "v"(vc + kr * D + cofs), "s"(mv)
-                 : "memory");
+                 :: "v"(kc + kr1 * D + cofs), "s"(mk + 1024u) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(vc + kr0 * D + cofs), "s"(mv) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(vc + kr1 * D + cofs), "s"(mv + 1024u) : "memory");
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
                  :: "v"(warr + wr * 2), "s"(mw) : "memory");
   };
 
   issue(0, 0);
-  issue(1, 1);
 
-  // ---- q of the wave's rows as MFMA B operands, pre-scaled (fp16), while the tiles fly
+  // ---- q of the wave's rows as MFMA B operands, pre-scaled (fp16), while the tile flies
   half8_t qb[2][4];
   int lim[2];  // causal bound of this lane's row per N tile (-1: not a row of the chunk)
 #pragma unroll
@@ -139,18 +143,16 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     lsum[nt] = 0.0f;
   }
 
-  // dequantization roles: K -- key dk = tid / 8, dims 16 dc .. 16 dc + 15; V -- the 8 keys of
-  // k-slot group u = wv (k-step u / 4, lane group u % 4) and dims 2 lane, 2 lane + 1
-  const int dk = tid >> 3, dc = tid & 7;
-  const int ve = wv >> 2, vq = wv & 3;
-
   for (int t = 0; t < T; ++t) {
-    const int slot = t % 3;
-    asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // tile t landed (t + 1's copies may fly)
+    const int slot = t & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile t landed
     __syncthreads();  // every wave's copies of tile t, and every wave done with tile t - 1
-    issue(t + 2, (t + 2) % 3);
+    issue(t + 1, slot ^ 1);  // lands while tile t is dequantized and computed
     const PrefillRaw& rw = sm.raw[slot];
-    {  // K: 16 codes of key dk
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // K: 16 codes of key dk, dims 16 dc .. 16 dc + 15
+      const int u = tid + 512 * i;
+      const int dk = u >> 3, dc = u & 7;
       const uint4 c4 = *reinterpret_cast<const uint4*>(rw.k + dk * D + 16 * dc);
       const int g = dc >> 2;
       const float s = g ? bf16_hi(rw.w[0][dk]) : bf16_lo(rw.w[0][dk]);
@@ -167,7 +169,10 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
       kd[(2 * dc) ^ (dk & 15)] = make_uint4(h[0], h[1], h[2], h[3]);
       kd[(2 * dc + 1) ^ (dk & 15)] = make_uint4(h[4], h[5], h[6], h[7]);
     }
-    {  // V: keys 32 ve + 16 hh + 4 vq + r (slot 8 vq + 4 hh + r of k-step ve), dims 2 lane, +1
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // V: slot group wv + 8 i (k-step ve, lane group vq), dims 2 lane, +1
+      const int grp = wv + 8 * i;
+      const int ve = grp >> 2, vq = grp & 3;
       const int g = lane >> 5;
       float lo[8], hi[8];
 #pragma unroll
@@ -183,10 +188,10 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
         }
       const int d0 = 2 * lane;
       const int chunk = 4 * ve + vq;  // slots 32 ve + 8 vq .. + 7
-      reinterpret_cast<uint4*>(sm.vt + d0 * PT)[chunk ^ ((d0 >> 1) & 7)] =
+      reinterpret_cast<uint4*>(sm.vt + d0 * PT)[chunk ^ (d0 & 15)] =
           make_uint4(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]), pack_h2(lo[4], lo[5]),
                      pack_h2(lo[6], lo[7]));
-      reinterpret_cast<uint4*>(sm.vt + (d0 + 1) * PT)[chunk ^ (((d0 + 1) >> 1) & 7)] =
+      reinterpret_cast<uint4*>(sm.vt + (d0 + 1) * PT)[chunk ^ ((d0 + 1) & 15)] =
           make_uint4(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]), pack_h2(hi[4], hi[5]),
                      pack_h2(hi[6], hi[7]));
     }
@@ -201,9 +206,9 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     // c: keys 16 mt + 4 lq4 + r of row 16 nt + lc (log2 units)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      f4_t c[4];
+      f4_t c[PMT];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < PMT; ++mt) {
         const int key = 16 * mt + lc;
         const uint4* kr = reinterpret_cast<const uint4*>(sm.k + key * D);
         c[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -214,24 +219,18 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
                                                          qb[nt][kk], c[mt], 0, 0, 0);
         }
       }
-      float s[4][4];
-      if (full) {
+      if (!full) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s[mt][r] = c[mt][r];
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < PMT; ++mt)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            s[mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? c[mt][r] : -INFINITY;
+            c[mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? c[mt][r] : -INFINITY;
       }
       float tmax = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < PMT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s[mt][r]);
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, c[mt][r]);
       tmax = max_xor16(tmax);
       tmax = max_xor32(tmax);
       const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
@@ -245,34 +244,28 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
       }
       const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float ls = 0.0f;
-      uint32_t pw[2][4];  // P.V B operands [k-step][dword]
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < PE; ++e) {
         float p[8];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            p[4 * hh + r] = __builtin_amdgcn_exp2f(s[2 * e + hh][r] - mref);
+            p[4 * hh + r] = __builtin_amdgcn_exp2f(c[2 * e + hh][r] - mref);
             ls += p[4 * hh + r];
           }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pw[e][j] = pack_h2(p[2 * j], p[2 * j + 1]);
-      }
-      lsum[nt] += ls;
-      // P.V: out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const half8_t pb = words_as_h8(pw[e][0], pw[e][1], pw[e][2], pw[e][3]);
+        const half8_t pb = words_as_h8(pack_h2(p[0], p[1]), pack_h2(p[2], p[3]),
+                                       pack_h2(p[4], p[5]), pack_h2(p[6], p[7]));
+        // P.V: out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           const int d = 16 * dt + lc;
-          const uint4 a =
-              reinterpret_cast<const uint4*>(sm.vt + d * PT)[(4 * e + lq4) ^ ((d >> 1) & 7)];
+          const uint4 a = reinterpret_cast<const uint4*>(sm.vt + d * PT)[(4 * e + lq4) ^ (d & 15)];
           oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(words_as_h8(a.x, a.y, a.z, a.w),
                                                                 pb, oacc[nt][dt], 0, 0, 0);
         }
       }
+      lsum[nt] += ls;
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end
