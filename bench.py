@@ -337,20 +337,23 @@ def run_workload(args):
         # dequantized copy). 4 rotating layer caches.
         from lagunalab_amd.q8_attn import q8_prefill_attention
         n, L, nl = args.ctx, 2048, 4
+        if n < L:
+            raise SystemExit(f"--ctx {n} must cover the {L}-row chunk")
         nc = n - L
         cap = (n + 255) // 256 * 256
         layers = []
         for _ in range(nl):
             lay = []
             for _kv in range(2):
-                x = torch.randn((1, HKV, nc, D), device=dev, generator=g).to(torch.bfloat16)
                 codes = torch.zeros((1, HKV, cap, D), dtype=torch.uint8, device=dev)
                 sc = torch.zeros((1, HKV, cap, 2), dtype=torch.bfloat16, device=dev)
                 bi = torch.zeros_like(sc)
-                _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, nc, D, codes.data_ptr(),
-                                                  sc.data_ptr(), bi.data_ptr(), cap, 0, 8, GS, sp),
-                           "prefill quantize")
-                del x
+                if nc:
+                    x = torch.randn((1, HKV, nc, D), device=dev, generator=g).to(torch.bfloat16)
+                    _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, nc, D, codes.data_ptr(),
+                                                      sc.data_ptr(), bi.data_ptr(), cap, 0, 8, GS,
+                                                      sp), "prefill quantize")
+                    del x
                 lay.append((codes, sc, bi))
             layers.append(lay)
         qv = torch.randn((1, HQ, L, D), device=dev, generator=g).to(torch.bfloat16)

@@ -62,7 +62,8 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   const int lq4 = lane >> 4;
   const int x = blockIdx.x;
   const int hk = x % Hkv;  // consecutive workgroups (consecutive XCDs) take consecutive KV heads
-  const int pb = (x / Hkv) % npb;
+  // last position blocks first: they see the most keys, so the dispatch order is longest first
+  const int pb = npb - 1 - (x / Hkv) % npb;
   const int b = x / (Hkv * npb);
   const int PB = PROWS / G;  // positions per workgroup
   const int Hq = Hkv * G;
