@@ -186,6 +186,25 @@ int lq_greedy_accept(const float* logits, int64_t L, int64_t V, const int32_t* d
                      void* stream);
 
 /*
+ * The fused decode step of a full-attention layer from raw projections: q (bf16 [B, Hq, 1, D]) and
+ * k_new are the rows before the layer's q_norm / k_norm and RoPE (laguna_mlx/laguna.py:97-101),
+ * which the attention kernel applies itself (norm weights bf16 [128], norm_eps; RoPE at the append
+ * row, inv_freq fp32 [rot_dims / 2], rot_dims a multiple of 4 up to 128, rotated dims scaled by
+ * mscale; the same arithmetic as lq_qk_norm_rope) before the fused append and attention of
+ * lq_q8_decode_append_attn. pos: as lq_q8_decode_append_attn_pos (device append rows), or null:
+ * every sequence appends at row n_plan. At most 4 query heads per KV head; workspace sized for
+ * n_plan + 1 rows.
+ */
+int lq_q8_decode_norm_append_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                  uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc,
+                                  uint16_t* vs, uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv,
+                                  int64_t D, int64_t cap, int64_t n_plan, const int32_t* pos,
+                                  const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                  float norm_eps, const float* inv_freq, int64_t rot_dims,
+                                  float mscale, float scale, uint16_t* out, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
+/*
  * lq_q8_decode_append_attn with the append rows read on the device: pos int32 [B] (device) is the
  * row each sequence appends at (its rows before the append), so that one recorded launch -- a HIP
  * graph of a decode step -- serves every step; the split plan and the workspace are those of

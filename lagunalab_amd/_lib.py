@@ -49,6 +49,9 @@ SIGNATURES = {
     "lq_add_rms_norm": (i32, [vp, vp, vp, vp, vp, i64, i64, f32, vp]),
     "lq_gemv_bf16": (i32, [vp, vp, vp, i64, i64, vp]),
     "lq_gemv_fused": (i32, [vp, vp, vp, vp, vp, i64, i64, i32, f32, i32, vp]),
+    "lq_q8_decode_norm_append_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64,
+                                            i64, i64, i64, vp, vp, vp, f32, vp, i64, f32, f32, vp,
+                                            vp, i64, vp]),
     "lq_q8_prefill_attn": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64,
                                  f32, vp, vp]),
     "lq_gemv_norm_rope": (i32, [vp, vp, vp, vp, i64, i64, f32, vp, vp, i64, i64, f32, vp, i64, f32,

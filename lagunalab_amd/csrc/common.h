@@ -187,4 +187,73 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// RMSNorm (times w, rounded to bf16) and RoPE at position `pos` of one 128-dim head row held by
+// one wave (the reference's q_norm / k_norm, then rope, laguna_mlx/laguna.py:97-101): lane l
+// holds dims 2l and 2l + 1 as the bf16 pair x2 (norm weights w2); returns the lane's output pair.
+// The normalized row is rounded to bf16 before the rotation, as the reference's two separate ops
+// round between them; the rotation is the non-interleaved form on the first rot_dims dims (dim i
+// pairs with dim i + rot_dims / 2, the partner value rot_dims / 4 lanes away), angle pos *
+// inv_freq[i], rotated dims scaled by mscale.
+// sin and cos of the fp32 angle a (|a| up to ~2^24): the reduction by 2 pi is done in fp64 (exact
+// to ~1e-11 for these magnitudes), so sincosf runs on |r| <= pi, its short path.
+__device__ __forceinline__ void sincos_reduced(float a, float* s, float* c) {
+  const double ad = (double)a;
+  const double k = rint(ad * 0.15915494309189535);      // 1 / (2 pi)
+  sincosf((float)fma(-k, 6.283185307179586, ad), s, c);  // 2 pi
+}
+
+// The value of lane (lane +- off) for rotation partners: whole-row swaps on the VALU for off 16
+// and 32 (the half- and full-rotary cases of head_dim 128), a cross-lane read otherwise. All 64
+// lanes must be active; lanes without a partner get an unspecified value.
+__device__ __forceinline__ float rope_partner(float y, int lane, int off, int partner) {
+  if (off == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+  }
+  if (off == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+  }
+  return __shfl(y, partner, 64);
+}
+
+__device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,
+                                                   const float* __restrict__ inv_freq,
+                                                   int rot_dims, float mscale, float pos) {
+  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
+  float ss = x0 * x0 + x1 * x1;  // sum over the wave: rows of 16 by DPP, then row swaps
+  ss += dpp<DPP_QUAD_XOR1>(ss);
+  ss += dpp<DPP_QUAD_XOR2>(ss);
+  ss += dpp<DPP_ROW_ROR4>(ss);
+  ss += dpp<DPP_ROW_ROR8>(ss);
+  ss = sum_xor32(sum_xor16(ss));
+  const float inv = rsqrtf(ss * (1.0f / 128) + eps);
+  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
+  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
+  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
+
+  const int half = rot_dims >> 1;      // rotated pairs
+  const int lane_off = rot_dims >> 2;  // partner lane distance
+  const bool rot = 2 * lane < rot_dims;
+  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
+  const float p0 = rope_partner(y0, lane, lane_off, partner);
+  const float p1 = rope_partner(y1, lane, lane_off, partner);
+  if (rot) {
+    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
+    const int i0 = first ? 2 * lane : 2 * lane - half;
+    float s0, c0, s1, c1;
+    sincos_reduced(pos * inv_freq[i0], &s0, &c0);
+    sincos_reduced(pos * inv_freq[i0 + 1], &s1, &c1);
+    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
+    if (first) {
+      y0 = a0 * c0 - b0 * s0;
+      y1 = a1 * c1 - b1 * s1;
+    } else {  // this lane holds x_{i+half}; the partner holds x_i
+      y0 = b0 * s0 + a0 * c0;
+      y1 = b1 * s1 + a1 * c1;
+    }
+  }
+  return (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+}
+
 }  // namespace lq

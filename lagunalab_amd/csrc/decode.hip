@@ -240,7 +240,8 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                 uint16_t* vs, uint16_t* vb, const uint16_t* k_new, const uint16_t* v_new,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                 const int32_t* lens, float scale, uint16_t* out, void* workspace,
-                int64_t workspace_bytes, hipStream_t st, const int32_t* pos_dev = nullptr) {
+                int64_t workspace_bytes, hipStream_t st, const int32_t* pos_dev = nullptr,
+                const AttnArgs* norm = nullptr) {
   LQ_CHECK_ARG(kind == LQ_KV_Q8 ||
                    ((kind == LQ_KV_BF16 || kind == LQ_KV_Q4) && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
                "kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
@@ -269,7 +270,19 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
   LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new && attn_merges_itself(Hq / Hkv)),
                "device positions need the fused 8-bit append with at most 4 query heads per KV head");
   AttnArgs a{};
+  LQ_CHECK_ARG(!norm || (kind == LQ_KV_Q8 && k_new && attn_merges_itself(Hq / Hkv)),
+               "the in-kernel q/k norm needs the fused 8-bit append with at most 4 query heads "
+               "per KV head");
   a.pos = pos_dev;
+  if (norm) {
+    a.qn_w = norm->qn_w;
+    a.kn_w = norm->kn_w;
+    a.inv_freq = norm->inv_freq;
+    a.rot_dims = norm->rot_dims;
+    a.mscale = norm->mscale;
+    a.norm_eps = norm->norm_eps;
+    kern.fn = q8_attn_norm_fn();
+  }
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);
   a.ks = ks;
@@ -345,6 +358,33 @@ extern "C" int lq_q8_decode_append_attn(const uint16_t* q, const uint16_t* k_new
   return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
                      n + 1, lens_host ? after : nullptr, scale, out, workspace, workspace_bytes,
                      (hipStream_t)stream);
+}
+
+extern "C" int lq_q8_decode_norm_append_attn(
+    const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new, uint8_t* kc, uint16_t* ks,
+    uint16_t* kb, uint8_t* vc, uint16_t* vs, uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv,
+    int64_t D, int64_t cap, int64_t n_plan, const int32_t* pos, const uint16_t* q_norm_w,
+    const uint16_t* k_norm_w, float norm_eps, const float* inv_freq, int64_t rot_dims,
+    float mscale, float scale, uint16_t* out, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(k_new && v_new && q_norm_w && k_norm_w && (inv_freq || rot_dims == 0),
+               "null pointer");
+  LQ_CHECK_ARG(rot_dims >= 0 && rot_dims <= 128 && rot_dims % 4 == 0,
+               "rot_dims must be a multiple of 4 in [0, 128] (got %lld)", (long long)rot_dims);
+  LQ_CHECK_ARG(n_plan >= 0 && n_plan < cap, "n_plan=%lld leaves no room to append in capacity %lld",
+               (long long)n_plan, (long long)cap);
+  AttnArgs norm{};
+  norm.qn_w = q_norm_w;
+  norm.kn_w = k_norm_w;
+  norm.inv_freq = inv_freq;
+  norm.rot_dims = (int)rot_dims;
+  norm.mscale = mscale;
+  norm.norm_eps = norm_eps;
+  return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
+                     n_plan + 1, nullptr, scale, out, workspace, workspace_bytes,
+                     (hipStream_t)stream, pos, &norm);
 }
 
 extern "C" int lq_q8_decode_append_attn_pos(const uint16_t* q, const uint16_t* k_new,

@@ -20,45 +20,6 @@ namespace {
 
 constexpr int ND = 128;  // head_dim
 
-// RMSNorm (times w, rounded to bf16) and RoPE at position `pos` of one head row held by one
-// wave: lane l holds dims 2l and 2l + 1 as the bf16 pair x2 (norm weights w2); returns the
-// lane's output pair.
-__device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,
-                                                   const float* __restrict__ inv_freq,
-                                                   int rot_dims, float mscale, float pos) {
-  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
-  float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  const float inv = 1.0f / sqrtf(ss * (1.0f / ND) + eps);
-  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
-  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
-  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
-
-  const int half = rot_dims >> 1;      // rotated pairs
-  const int lane_off = rot_dims >> 2;  // partner lane distance
-  const bool rot = 2 * lane < rot_dims;
-  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
-  const float p0 = __shfl(y0, partner, 64);
-  const float p1 = __shfl(y1, partner, 64);
-  if (rot) {
-    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
-    const int i0 = first ? 2 * lane : 2 * lane - half;
-    float s0, c0, s1, c1;
-    sincosf(pos * inv_freq[i0], &s0, &c0);
-    sincosf(pos * inv_freq[i0 + 1], &s1, &c1);
-    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
-    if (first) {
-      y0 = a0 * c0 - b0 * s0;
-      y1 = a1 * c1 - b1 * s1;
-    } else {  // this lane holds x_{i+half}; the partner holds x_i
-      y0 = b0 * s0 + a0 * c0;
-      y1 = b1 * s1 + a1 * c1;
-    }
-  }
-  return (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
-}
-
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_out, const uint16_t* __restrict__ q_w,

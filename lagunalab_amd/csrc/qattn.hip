@@ -61,10 +61,19 @@ struct PackSmem {
   alignas(16) float st[NWAVE][4][6];
 };
 
-template <bool CAUSAL>
+// The NORM variant's extra staging (RoPE frequencies of each wave's copy).
+template <bool NORM>
+struct PackNormSmem {
+  alignas(16) float inv_freq[NWAVE][64];
+};
+template <>
+struct PackNormSmem<false> {};
+
+template <bool CAUSAL, bool NORM = false>
 __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
     AttnArgs args, DecodePlan plan) {
   __shared__ PackSmem sm;
+  __shared__ PackNormSmem<NORM> nsm;
   __shared__ int sh_last;
   const uint16_t* __restrict__ q = args.q;
   const uint8_t* __restrict__ kc = args.kc;
@@ -356,11 +365,37 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       dma_b32<1024>(args.knew + src, 4u * (uint32_t)lane, stage);
       dma_b32<1280>(args.vnew + src, 4u * (uint32_t)lane, stage);
     }
+    if constexpr (NORM) {  // norm weights behind the new rows, RoPE frequencies beside
+      dma_b32<1536>(args.qn_w, 4u * (uint32_t)lane, stage);
+      dma_b32<1792>(args.kn_w, 4u * (uint32_t)lane, stage);
+      const int nf = args.rot_dims >> 1;  // wave-uniform; without rotation re-read the q weights
+      dma_b32<0>(nf ? (const void*)args.inv_freq : (const void*)args.qn_w,
+                 4u * (uint32_t)min(lane, max(nf, 1) - 1), lds_addr(&nsm.inv_freq[wv][0]));
+    }
   }
   issue(cur, B0);
   grab(g, 2 >= NS);  // super-tile number 2: dynamic when NS == 2
   issue(nxt, B1);
   asm volatile("s_waitcnt vmcnt(41)" ::: "memory");  // the q and new rows have landed
+  if constexpr (NORM) {
+    // Raw q rows and new K row -> RMSNorm + RoPE at position n - 1. Row j (q rows 0 .. R - 1, the
+    // K row as j = R) is done by wave j % NWAVE from its own staged copy and written into every
+    // wave's copy; the barriers order the copies' landing and the writes.
+    __syncthreads();  // every wave's staged rows have landed (each waited for its own above)
+    const uint8_t* own = reinterpret_cast<const uint8_t*>(&tm);
+    const float pos = (float)(n - 1);
+    for (int j = wv; j <= R; j += NWAVE) {  // wave-uniform
+      const int off = j < R ? j * 2 * D : 1024;
+      const uint32_t w2 = reinterpret_cast<const uint32_t*>(own + (j < R ? 1536 : 1792))[lane];
+      const uint32_t y = norm_rope_lane(reinterpret_cast<const uint32_t*>(own + off)[lane], w2,
+                                        lane, args.norm_eps, &nsm.inv_freq[wv][0], args.rot_dims,
+                                        args.mscale, pos);
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w)
+        reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(&sm.loop.terms[w]) + off)[lane] = y;
+    }
+    __syncthreads();
+  }
 
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
   {
@@ -467,5 +502,7 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
 QAttnFn q8_attn_fn(bool causal) {
   return causal ? q8_attn_packed_kernel<true> : q8_attn_packed_kernel<false>;
 }
+
+QAttnFn q8_attn_norm_fn() { return q8_attn_packed_kernel<false, true>; }
 
 }  // namespace lq

@@ -10,7 +10,7 @@ not part of this path.
 The host (Python, ctypes) takes longer to issue a step's launches than the GPU to run them.
 :meth:`DecodeStack.capture` records the whole step once into a HIP graph
 (``torch.cuda.CUDAGraph``) whose launches read the token position from device memory: the RoPE
-position and the fused decode step's append row (``lq_q8_decode_append_attn_pos``) come from one
+position and the fused decode step's append row (``lq_q8_decode_norm_append_attn``) come from one
 int32 counter that the graph's last launch increments, so each replay decodes the next token. The
 caches' buffers are reserved for the replays beforehand (a replay never grows them) and their host
 offsets advance after each replay.
@@ -52,9 +52,10 @@ class DecodeStack:
     (``DequantKVCache(fused_decode=True)``, one sequence, equal offsets) of the layers in order.
 
     A layer of a step is three launches: the input projection with the layer's input RMSNorm in
-    its prologue and the q/k RMSNorm + RoPE of each head in its epilogue (``lq_gemv_norm_rope``),
-    the fused decode step, and the output projection with the softplus gate in its prologue and
-    the residual add in its epilogue (``lq_gemv_fused`` mode 2). :meth:`step` issues them from
+    its prologue (``lq_gemv_fused`` mode 1), the fused decode step from the raw q and new K rows
+    (``lq_q8_decode_norm_append_attn``: q/k RMSNorm + RoPE in the attention kernel's prologue,
+    while its first tiles stream in), and the output projection with the softplus gate in its
+    prologue and the residual add in its epilogue (``lq_gemv_fused`` mode 2). :meth:`step` issues them from
     the host; :meth:`capture` records them once into a HIP graph that :meth:`replay` runs per
     token."""
 
@@ -68,46 +69,35 @@ class DecodeStack:
         self.blocks, self.norms, self.caches, self.eps = blocks, norms, caches, eps
         self.graph = None
         self.pos = None
-        self._cnt = None
-
-    def _counters(self, dev, n):
-        """Arrival counters of the input projection's head epilogue (zero between launches; the
-        launches of all layers share them, one after another on one stream)."""
-        if self._cnt is None or self._cnt.numel() < n:
-            self._cnt = torch.zeros(n, dtype=torch.int32, device=dev)
-        return self._cnt.data_ptr()
 
     def _layer(self, blk: Attention, wn, cache, h, ws=None, n_plan=None):
         """One layer on the residual stream h [1, 1, C] (updated in place). Host mode (``ws`` None):
         the cache reserves the row and the fused step gets its length from the host; graph mode:
         positions from ``self.pos``, workspace ``ws`` and plan length ``n_plan``."""
-        from .q8_attn import decode_append_attention
+        from .q8_attn import _workspace
         lib = _lib.load()
         dev = h.device
         sp = _lib.stream_ptr(dev)
         H, Hkv, D = blk.n_heads, blk.n_kv_heads, blk.head_dim
         proj = torch.empty((1, 1, blk.w_in.shape[0]), dtype=torch.bfloat16, device=dev)
+        _gemv_fused(blk.w_in, h, wn, None, proj, 1, self.eps)
         q, k, v, g = torch.split(proj, blk._splits, dim=-1)  # contiguous pieces of one row
-        q4, k4, v4 = (t.view(1, hh, 1, D) for t, hh in ((q, H), (k, Hkv), (v, Hkv)))
         host = ws is None
-        row = cache.q.reserve(k4, v4) if host else 0
-        _lib.check(lib.lq_gemv_norm_rope(
-            blk.w_in.data_ptr(), h.data_ptr(), wn.data_ptr(), proj.data_ptr(), blk.w_in.shape[0],
-            blk.w_in.shape[1], float(self.eps), blk.q_norm.data_ptr(), blk.k_norm.data_ptr(), H,
-            Hkv, float(blk.eps), blk.inv_freq.data_ptr(), blk.rot_dims, float(blk.mscale),
-            int(row), None if host else self.pos.data_ptr(), self._counters(dev, H + Hkv),
-            sp), "lq_gemv_norm_rope")
-        if host:
-            out = decode_append_attention(q4, k4, v4, cache.q.keys, cache.q.values, n=row,
-                                          scale=blk.scale)
-        else:
-            (kc, ks, kb), (vc, vs, vb) = cache.q.keys, cache.q.values
-            out = torch.empty((1, H, 1, D), dtype=torch.bfloat16, device=dev)
-            _lib.check(lib.lq_q8_decode_append_attn_pos(
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), ks.data_ptr(),
-                kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, H, Hkv, D,
-                kc.shape[2], n_plan, self.pos.data_ptr(), float(blk.scale), out.data_ptr(),
-                ws.data_ptr(), ws.numel(), sp), "lq_q8_decode_append_attn_pos")
+        if host:  # the cache reserves the row; the kernel writes it
+            n_plan = cache.q.reserve(k.view(1, Hkv, 1, D), v.view(1, Hkv, 1, D))
+            nb = lib.lq_decode_workspace_bytes(_lib.LQ_KV_Q8, 1, H, Hkv, D, n_plan + 1, None)
+            if nb < 0:
+                raise ValueError(lib.lq_last_error().decode())
+            ws = _workspace(dev, nb)
+        (kc, ks, kb), (vc, vs, vb) = cache.q.keys, cache.q.values
+        out = torch.empty((1, H, 1, D), dtype=torch.bfloat16, device=dev)
+        _lib.check(lib.lq_q8_decode_norm_append_attn(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+            vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, H, Hkv, D, kc.shape[2], int(n_plan),
+            None if host else self.pos.data_ptr(), blk.q_norm.data_ptr(), blk.k_norm.data_ptr(),
+            float(blk.eps), blk.inv_freq.data_ptr(), blk.rot_dims, float(blk.mscale),
+            float(blk.scale), out.data_ptr(), ws.data_ptr(), ws.numel(), sp),
+            "lq_q8_decode_norm_append_attn")
         _gemv_fused(blk.wo, out, g, h, h, 2, self.eps, 0 if blk.per_head_gate else 1)
 
     def step(self, x: torch.Tensor) -> torch.Tensor:
@@ -153,7 +143,6 @@ class DecodeStack:
             if nb < 0:
                 raise ValueError(lib.lq_last_error().decode())
             self.ws.append(torch.zeros(nb, dtype=torch.uint8, device=dev))  # counters start at 0
-        self._counters(dev, max(b.n_heads + b.n_kv_heads for b in self.blocks))
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):

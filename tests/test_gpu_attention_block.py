@@ -242,6 +242,65 @@ def test_gemv_norm_rope_equals_two_launches(dev, H, Hkv, C, rot, device_pos):
         assert int(cnt.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("G,B,rot,device_pos", [(4, 1, 64, True), (4, 1, 128, False),
+                                                (2, 2, 0, True), (4, 2, 64, False)])
+def test_decode_norm_entry_equals_norm_then_decode(dev, G, B, rot, device_pos):
+    """lq_q8_decode_norm_append_attn (q/k RMSNorm + RoPE inside the attention kernel) equals
+    lq_qk_norm_rope followed by the fused decode step, bit for bit: output and cache bytes; host
+    append row or device positions, partial / full / no rotation, one and two sequences."""
+    from lagunalab_amd import _lib
+    from lagunalab_amd.attention import rope_frequencies
+    from lagunalab_amd.quant import quantize_kv_into
+    lib = _lib.load()
+    rng = np.random.default_rng(70 + G + B + rot)
+    Hkv, n, cap = 8, 3000, 3072
+    H = Hkv * G
+    k0, v0 = _bf16(rng, (B, Hkv, n, 128)), _bf16(rng, (B, Hkv, n, 128))
+    mk = lambda: tuple(torch.zeros(sh, dtype=dt, device=dev) for sh, dt in (
+        ((B, Hkv, cap, 128), torch.uint8), ((B, Hkv, cap, 2), torch.bfloat16),
+        ((B, Hkv, cap, 2), torch.bfloat16)))
+    ka, va = mk(), mk()
+    quantize_kv_into(k0, v0, ka, va, 0)
+    kb_, vb_ = tuple(t.clone() for t in ka), tuple(t.clone() for t in va)
+    params = {"rope_type": "yarn", "rope_theta": 5e5, "factor": 32.0,
+              "original_max_position_embeddings": 4096, "partial_rotary_factor": rot / 128}
+    inv, rot_dims, mscale = rope_frequencies(128, params) if rot else (torch.ones(1), 0, 1.0)
+    inv = inv.to(dev)
+    qn, kn = _bf16(rng, (128,), 0.1) + 1, _bf16(rng, (128,), 0.1) + 1
+    nb = lib.lq_decode_workspace_bytes(_lib.LQ_KV_Q8, B, H, Hkv, 128, n + 3, None)
+    wa = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    wb = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    sp = _lib.stream_ptr(dev)
+    pos = torch.full((B,), n, dtype=torch.int32, device=dev)
+    for step in range(3):
+        q = _bf16(rng, (B, H, 1, 128), 3.0)
+        k1, v1 = _bf16(rng, (B, Hkv, 1, 128), 3.0), _bf16(rng, (B, Hkv, 1, 128))
+        # reference: separate norm + rope launch, then the fused decode step
+        qr, kr = q.clone(), k1.clone()
+        _lib.check(lib.lq_qk_norm_rope(qr.data_ptr(), kr.data_ptr(), qr.data_ptr(), kr.data_ptr(),
+                                       qn.data_ptr(), kn.data_ptr(), B, H, Hkv, 1, 128, 1e-6,
+                                       inv.data_ptr(), rot_dims, mscale, n + step, None, sp), "rope")
+        want = torch.empty((B, H, 1, 128), dtype=torch.bfloat16, device=dev)
+        (kc, ks, kb), (vc, vs, vb) = ka, va
+        _lib.check(lib.lq_q8_decode_append_attn_pos(
+            qr.data_ptr(), kr.data_ptr(), v1.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+            vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, H, Hkv, 128, cap, n + step,
+            pos.data_ptr(), 0.09, want.data_ptr(), wa.data_ptr(), wa.numel(), sp), "decode")
+        got = torch.empty_like(want)
+        (kc, ks, kb), (vc, vs, vb) = kb_, vb_
+        _lib.check(lib.lq_q8_decode_norm_append_attn(
+            q.data_ptr(), k1.data_ptr(), v1.data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+            vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, H, Hkv, 128, cap,
+            n if device_pos else n + step, pos.data_ptr() if device_pos else None, qn.data_ptr(),
+            kn.data_ptr(), 1e-6, inv.data_ptr(), rot_dims, mscale, 0.09, got.data_ptr(),
+            wb.data_ptr(), wb.numel(), sp), "norm decode")
+        pos.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), step
+        for x, y in zip(ka + va, kb_ + vb_):
+            assert torch.equal(x, y), step
+
+
 def test_add_rms_norm_matches_restatement(dev):
     from lagunalab_amd.decoder import add_rms_norm
     rng = np.random.default_rng(21)
