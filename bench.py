@@ -490,9 +490,10 @@ def run_workload(args):
     if args.workload == "layers":
         # One decoded token through the attention blocks of the model's full-attention layers
         # (laguna.py:94-111 per layer, with the layer's input RMSNorm and residual add), three
-        # launches per layer: the q/k/v/gate projection with the input RMSNorm before it and the
-        # q/k RMSNorm + RoPE (YaRN, partial rotary 0.5) after it, the fused decode step over the
-        # layer's 8-bit cache, o_proj with the softplus gate before it and the residual add after.
+        # launches per layer: the q/k/v/gate projection with the input RMSNorm before it, the
+        # fused decode step over the layer's 8-bit cache with the q/k RMSNorm + RoPE (YaRN,
+        # partial rotary 0.5) in its prologue, o_proj with the softplus gate before it and the
+        # residual add after.
         # Synthetic bf16 weights N(0, 0.02), caches of 82,671 quantized N(0,1) rows per layer.
         # Timed as one HIP graph replay per token (positions on the device); the eager step is
         # timed beside it.
@@ -552,8 +553,8 @@ def run_workload(args):
                  "bytes_per_token": {"kv": kv_bytes, "weights": w_bytes},
                  "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
                               "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
-                              "kernel": f"one HIP graph per token: {nl} x (lq_gemv_norm_rope, "
-                                        "lq_q8_decode_append_attn_pos, lq_gemv_fused)",
+                              "kernel": f"one HIP graph per token: {nl} x (lq_gemv_fused, "
+                                        "lq_q8_decode_norm_append_attn, lq_gemv_fused)",
                               "bytes_per_call": nbytes}}
         _result(f"attention blocks of {nl} full-attention layers, us per decoded token at "
                 f"{n0}-token ctx", round(ms * 1e3, 2), "us/token", False, ms, args, "u8",
