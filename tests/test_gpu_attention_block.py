@@ -242,18 +242,20 @@ def test_gemv_norm_rope_equals_two_launches(dev, H, Hkv, C, rot, device_pos):
         assert int(cnt.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("G,B,rot,device_pos", [(4, 1, 64, True), (4, 1, 128, False),
-                                                (2, 2, 0, True), (4, 2, 64, False)])
-def test_decode_norm_entry_equals_norm_then_decode(dev, G, B, rot, device_pos):
+@pytest.mark.parametrize("G,B,rot,device_pos,n", [(4, 1, 64, True, 3000), (4, 1, 128, False, 3000),
+                                                  (2, 2, 0, True, 3000), (4, 2, 64, False, 3000),
+                                                  (4, 1, 64, True, 7), (1, 1, 128, False, 70)])
+def test_decode_norm_entry_equals_norm_then_decode(dev, G, B, rot, device_pos, n):
     """lq_q8_decode_norm_append_attn (q/k RMSNorm + RoPE inside the attention kernel) equals
     lq_qk_norm_rope followed by the fused decode step, bit for bit: output and cache bytes; host
-    append row or device positions, partial / full / no rotation, one and two sequences."""
+    append row or device positions, partial / full / no rotation, one and two sequences, G = 1, 2,
+    4, and short caches where most waves have no super-tile."""
     from lagunalab_amd import _lib
     from lagunalab_amd.attention import rope_frequencies
     from lagunalab_amd.quant import quantize_kv_into
     lib = _lib.load()
-    rng = np.random.default_rng(70 + G + B + rot)
-    Hkv, n, cap = 8, 3000, 3072
+    rng = np.random.default_rng(70 + G + B + rot + n)
+    Hkv, cap = 8, 3072
     H = Hkv * G
     k0, v0 = _bf16(rng, (B, Hkv, n, 128)), _bf16(rng, (B, Hkv, n, 128))
     mk = lambda: tuple(torch.zeros(sh, dtype=dt, device=dev) for sh, dt in (
