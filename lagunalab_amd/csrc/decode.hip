@@ -241,7 +241,7 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t n,
                 const int32_t* lens, float scale, uint16_t* out, void* workspace,
                 int64_t workspace_bytes, hipStream_t st, const int32_t* pos_dev = nullptr,
-                const AttnArgs* norm = nullptr) {
+                const NormArgs* norm = nullptr) {
   LQ_CHECK_ARG(kind == LQ_KV_Q8 ||
                    ((kind == LQ_KV_BF16 || kind == LQ_KV_Q4) && Hkv >= 1 && Hq / Hkv <= 4 && !k_new),
                "kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
@@ -274,15 +274,6 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
                "the in-kernel q/k norm needs the fused 8-bit append with at most 4 query heads "
                "per KV head");
   a.pos = pos_dev;
-  if (norm) {
-    a.qn_w = norm->qn_w;
-    a.kn_w = norm->kn_w;
-    a.inv_freq = norm->inv_freq;
-    a.rot_dims = norm->rot_dims;
-    a.mscale = norm->mscale;
-    a.norm_eps = norm->norm_eps;
-    kern.fn = q8_attn_norm_fn();
-  }
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);
   a.ks = ks;
@@ -304,7 +295,10 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
   a.G = (int)(Hq / Hkv);
   a.L = 1;
   a.qk_scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(kern.fn, dim3((unsigned)S, (unsigned)Hkv), dim3((unsigned)kern.threads), 0,
+  if (norm)
+    launch_q8_attn_norm((unsigned)S, (unsigned)Hkv, st, a, plan, *norm);
+  else
+    hipLaunchKernelGGL(kern.fn, dim3((unsigned)S, (unsigned)Hkv), dim3((unsigned)kern.threads), 0,
                      st, a, plan);
   LQ_CHECK_LAUNCH("attention kernel");
   if (!fused_merge) {
@@ -375,7 +369,7 @@ extern "C" int lq_q8_decode_norm_append_attn(
                "rot_dims must be a multiple of 4 in [0, 128] (got %lld)", (long long)rot_dims);
   LQ_CHECK_ARG(n_plan >= 0 && n_plan < cap, "n_plan=%lld leaves no room to append in capacity %lld",
                (long long)n_plan, (long long)cap);
-  AttnArgs norm{};
+  NormArgs norm{};
   norm.qn_w = q_norm_w;
   norm.kn_w = k_norm_w;
   norm.inv_freq = inv_freq;

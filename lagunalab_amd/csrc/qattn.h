@@ -42,15 +42,6 @@ struct AttnArgs {
   // row sequence b appends at; its length is then pos[b] + 1 (clamped to [1, cap]) instead of
   // the plan's len[b], so that a launch recorded in a HIP graph serves every decode step.
   const int32_t* pos;
-  // q/k RMSNorm + RoPE inside the kernel (packed kernel's fused append with L = 1, the NORM
-  // variant only): the staged q rows and new K row are raw projections, normalized (weights qn_w /
-  // kn_w, bf16 [128], epsilon norm_eps) and rotated at position len - 1 (inv_freq fp32
-  // [rot_dims / 2], rotated dims scaled by mscale) before use.
-  const uint16_t* qn_w;
-  const uint16_t* kn_w;
-  const float* inv_freq;
-  int rot_dims;
-  float mscale, norm_eps;
   float* part_acc;    // workspace: split partials
   float2* part_ml;
   uint32_t* counters; // workspace: arrival and tile counters (zero between calls)
@@ -78,8 +69,21 @@ __host__ __device__ inline uint32_t* arrival_counter(uint32_t* counters, int i) 
 // Packed 8-bit kernel (qattn.hip) for G * L <= 4 query rows per KV head, causal for multi-row
 // verify blocks; it also merges the splits (no decode_merge_kernel launch).
 QAttnFn q8_attn_fn(bool causal);
-// The decode variant (no causal mask) whose prologue applies the q/k RMSNorm + RoPE of AttnArgs.
-QAttnFn q8_attn_norm_fn();
+// q/k RMSNorm + RoPE inside the packed kernel (fused append with L = 1): the staged q rows and
+// new K row are raw projections, normalized (weights qn_w / kn_w, bf16 [128], epsilon norm_eps)
+// and rotated at position len - 1 (inv_freq fp32 [rot_dims / 2], rotated dims scaled by mscale)
+// before use. A separate argument of that variant only, so that the other kernels' argument
+// blocks stay as they are.
+struct NormArgs {
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  const float* inv_freq;
+  int rot_dims;
+  float mscale, norm_eps;
+};
+// Launches the decode variant (no causal mask) with the in-kernel q/k norm on an S x Hkv grid.
+void launch_q8_attn_norm(unsigned S, unsigned Hkv, hipStream_t st, const AttnArgs& a,
+                         const DecodePlan& plan, const NormArgs& nargs);
 // Dense-layout kernel (attn_dense.hip) for 4 < G * L <= 16 nt rows per KV head; partials merged
 // by decode_merge_kernel.
 QAttnFn q8_dense_attn_fn(int nt, bool causal);

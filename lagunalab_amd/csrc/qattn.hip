@@ -69,9 +69,9 @@ struct PackNormSmem {
 template <>
 struct PackNormSmem<false> {};
 
-template <bool CAUSAL, bool NORM = false>
-__global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
-    AttnArgs args, DecodePlan plan) {
+template <bool CAUSAL, bool NORM>
+__device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const DecodePlan& plan,
+                                                    const NormArgs& nargs) {
   __shared__ PackSmem sm;
   __shared__ PackNormSmem<NORM> nsm;
   __shared__ int sh_last;
@@ -366,10 +366,10 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       dma_b32<1280>(args.vnew + src, 4u * (uint32_t)lane, stage);
     }
     if constexpr (NORM) {  // norm weights behind the new rows, RoPE frequencies beside
-      dma_b32<1536>(args.qn_w, 4u * (uint32_t)lane, stage);
-      dma_b32<1792>(args.kn_w, 4u * (uint32_t)lane, stage);
-      const int nf = args.rot_dims >> 1;  // wave-uniform; without rotation re-read the q weights
-      dma_b32<0>(nf ? (const void*)args.inv_freq : (const void*)args.qn_w,
+      dma_b32<1536>(nargs.qn_w, 4u * (uint32_t)lane, stage);
+      dma_b32<1792>(nargs.kn_w, 4u * (uint32_t)lane, stage);
+      const int nf = nargs.rot_dims >> 1;  // wave-uniform; without rotation re-read the q weights
+      dma_b32<0>(nf ? (const void*)nargs.inv_freq : (const void*)nargs.qn_w,
                  4u * (uint32_t)min(lane, max(nf, 1) - 1), lds_addr(&nsm.inv_freq[wv][0]));
     }
   }
@@ -388,8 +388,8 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
       const int off = j < R ? j * 2 * D : 1024;
       const uint32_t w2 = reinterpret_cast<const uint32_t*>(own + (j < R ? 1536 : 1792))[lane];
       const uint32_t y = norm_rope_lane(reinterpret_cast<const uint32_t*>(own + off)[lane], w2,
-                                        lane, args.norm_eps, &nsm.inv_freq[wv][0], args.rot_dims,
-                                        args.mscale, pos);
+                                        lane, nargs.norm_eps, &nsm.inv_freq[wv][0], nargs.rot_dims,
+                                        nargs.mscale, pos);
 #pragma unroll
       for (int w = 0; w < NWAVE; ++w)
         reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(&sm.loop.terms[w]) + off)[lane] = y;
@@ -497,12 +497,25 @@ __global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(
                        &sm.st[0][0][0], &sh_last, args, plan, x, b, hk, R);
 }
 
+template <bool CAUSAL>
+__global__ __launch_bounds__(NTHR) void q8_attn_packed_kernel(AttnArgs args, DecodePlan plan) {
+  q8_attn_packed_body<CAUSAL, false>(args, plan, NormArgs{});
+}
+
+__global__ __launch_bounds__(NTHR) void q8_attn_norm_kernel(AttnArgs args, DecodePlan plan,
+                                                           NormArgs nargs) {
+  q8_attn_packed_body<false, true>(args, plan, nargs);
+}
+
 }  // namespace
 
 QAttnFn q8_attn_fn(bool causal) {
   return causal ? q8_attn_packed_kernel<true> : q8_attn_packed_kernel<false>;
 }
 
-QAttnFn q8_attn_norm_fn() { return q8_attn_packed_kernel<false, true>; }
+void launch_q8_attn_norm(unsigned S, unsigned Hkv, hipStream_t st, const AttnArgs& a,
+                         const DecodePlan& plan, const NormArgs& nargs) {
+  q8_attn_norm_kernel<<<dim3(S, Hkv), dim3(NTHR), 0, st>>>(a, plan, nargs);
+}
 
 }  // namespace lq
