@@ -67,44 +67,86 @@ def parse():
     return p.parse_args()
 
 
-def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, seconds):
-    """The reference's unfused path restated by the oracle: dequantize the cache to bf16, then
-    fp32 SDPA (BLAS). The 8 KV heads run in a thread pool (NumPy releases the GIL)."""
-    import numpy as np
-    from concurrent.futures import ThreadPoolExecutor
+def cpu_threads():
+    """(worker threads, host cores) of the CPU baselines: every core this process may run on,
+    capped at the OMP_NUM_THREADS share when that is set (the per-GPU CPU share of a box)."""
+    host = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    return (max(1, min(host, int(share))) if share.isdigit() else host), host
 
-    from oracle import attention as A
+
+def cpu_attention(pool, q, k, v, n, scale, bits=8, causal=False, chunk=4096):
+    """The reference's unfused path (dequantize to bf16, fp32 SDPA) on the host cores: one task
+    per (KV head, chunk of keys) on ``pool`` -- the chunk dequantized by the oracle (bf16-rounded
+    ``scale * code + bias``), fp32 scores and weights with BLAS, the chunk's (max, sum, weighted V)
+    -- then the log-sum-exp merge per head. q fp32 [Hq, L, D]; k, v (codes [Hkv, cap, .], scale
+    and bias bf16 bits [Hkv, cap, D / 64]) or fp32 [Hkv, cap, D] values (``bits`` None); causal:
+    query row i at position n - L + i. Returns fp32 [Hq, L, D]."""
+    import numpy as np
+
     from oracle import quantize as Q
 
-    threads = min(HKV, len(os.sched_getaffinity(0)))
-    G = HQ // HKV
+    Hq, L, _ = q.shape
+    Hkv = (k[0] if isinstance(k, tuple) else k).shape[0]
+    G = Hq // Hkv
+    row = n - L + np.arange(G * L) % L
 
-    def one_head(h):
-        k = Q.dequantize(kc[h, :n], ks[h, :n], kb[h, :n])
-        v = Q.dequantize(vc[h, :n], vs[h, :n], vb[h, :n])
-        return A.sdpa(q[None, h * G:(h + 1) * G, None], k[None, None], v[None, None], D ** -0.5,
-                      dtype=np.float32)
+    def task(t):
+        h, a = t
+        e = min(a + chunk, n)
+        if bits is None:
+            kk, vv = k[h, a:e], v[h, a:e]
+        else:
+            kk = Q.dequantize(k[0][h, a:e], k[1][h, a:e], k[2][h, a:e], GS, bits)
+            vv = Q.dequantize(v[0][h, a:e], v[1][h, a:e], v[2][h, a:e], GS, bits)
+        s = (q[h * G:(h + 1) * G].reshape(G * L, D) @ kk.T) * np.float32(scale)
+        if causal and L > 1:
+            s = np.where(np.arange(a, e)[None, :] <= row[:, None], s, np.float32(-np.inf))
+        m = s.max(axis=-1)
+        ms = np.where(np.isfinite(m), m, np.float32(0))
+        p = np.exp(s - ms[:, None])
+        return h, m, p.sum(axis=-1), p @ vv
 
-    times = []
-    with ThreadPoolExecutor(threads) as ex:
-        list(ex.map(one_head, range(HKV)))  # warm-up
-        t_end = time.perf_counter() + seconds
-        while len(times) < 3 or time.perf_counter() < t_end:
-            t0 = time.perf_counter()
-            list(ex.map(one_head, range(HKV)))
-            times.append(time.perf_counter() - t0)
-    calls = len(times)
-    t = sorted(times)[len(times) // 2]
-    try:
-        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
-    except Exception:
-        model = "unknown"
+    parts = list(pool.map(task, [(h, a) for h in range(Hkv) for a in range(0, n, chunk)]))
+    out = np.empty((Hq, L, D), np.float32)
+    for h in range(Hkv):
+        mine = [x for x in parts if x[0] == h]
+        m = np.stack([x[1] for x in mine])
+        M = m.max(axis=0)
+        w = np.where(np.isfinite(m), np.exp(m - M), 0).astype(np.float32)
+        den = (w * np.stack([x[2] for x in mine])).sum(axis=0)
+        acc = (w[..., None] * np.stack([x[3] for x in mine])).sum(axis=0)
+        out[h * G:(h + 1) * G] = (acc / den[:, None]).reshape(G, L, D)
+    return out
+
+
+def time_cpu_attention(q, k, v, n, scale, seconds, bits=8, causal=False, min_calls=3):
+    """Median wall time of :func:`cpu_attention` on all worker threads (one BLAS thread each),
+    after one warm-up, repeated for about ``seconds``; returns (seconds per call, calls, threads,
+    host cores)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    threads, host = cpu_threads()
+    with threadpool_limits(limits=1), ThreadPoolExecutor(threads) as pool:
+        t, calls = _time_cpu(lambda: cpu_attention(pool, q, k, v, n, scale, bits, causal),
+                             seconds, min_calls)
+    return t, calls, threads, host
+
+
+def cpu_baseline(kc, ks, kb, vc, vs, vb, q, n, seconds):
+    """The reference's unfused path restated by the oracle, on all host cores
+    (:func:`cpu_attention`): one decode step's attention over one layer at n keys."""
+    t, calls, threads, host = time_cpu_attention(q.reshape(HQ, 1, D), (kc, ks, kb), (vc, vs, vb),
+                                                 n, D ** -0.5, seconds)
     return {
         "value": round(Q8_TOKEN * n / t / 1e9, 3), "unit": "GB/s", "cores": threads,
-        "kind": "port", "us_per_call": round(t * 1e6, 1),
+        "host_cores": host, "blas_threads": 1, "kind": "port", "us_per_call": round(t * 1e6, 1),
         "sample": (f"median of {calls} calls (after 1 warm-up) of the unfused dequantize-to-bf16 + "
-                   f"fp32 SDPA path at n={n} on one layer, 8 KV heads over {threads} threads; "
-                   f"CPU: {model}"),
+                   f"fp32 SDPA path at n={n} on one layer: (KV head, 4,096-key chunk) tasks on "
+                   f"{threads} worker threads with one BLAS thread each ({host} host cores); "
+                   f"CPU: {_cpu_model()}"),
     }
 
 
@@ -244,26 +286,27 @@ def run_workload(args):
                               "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
                               "kernel": f"lq_decode_attn ({name})", "bytes_per_call": nbytes}}
         if do_cpu:
-            from oracle import attention as A
-            from oracle import quantize as Q
             cv = lambda t: (t.cpu().numpy() if t.dtype == torch.uint8
                             else t.cpu().view(torch.int16).numpy().view(np.uint16))
-            qn = qs[0].float().cpu().numpy()
+            qn = qs[0, 0].float().cpu().numpy()  # [HQ, 1, D]
             if kind == _lib.LQ_KV_Q4:
-                kh = tuple(cv(t)[:, :, :n] for t in layers[0][0])
-                vh = tuple(cv(t)[:, :, :n] for t in layers[0][1])
-                fn = lambda: A.sdpa(qn, Q.dequantize(*kh, GS, 4), Q.dequantize(*vh, GS, 4), scale,
-                                    dtype=np.float32)
+                kh = tuple(cv(t)[0] for t in layers[0][0])
+                vh = tuple(cv(t)[0] for t in layers[0][1])
+                t, calls, threads, host = time_cpu_attention(qn, kh, vh, n, scale, args.cpu_seconds,
+                                                             bits=4)
             else:
-                kf = layers[0][0][0][:, :, :n].float().cpu().numpy()
-                vf = layers[0][1][0][:, :, :n].float().cpu().numpy()
-                fn = lambda: A.sdpa(qn, kf, vf, scale, dtype=np.float32)
-            t, calls = _time_cpu(fn, args.cpu_seconds)
+                kf = layers[0][0][0][0].float().cpu().numpy()
+                vf = layers[0][1][0][0].float().cpu().numpy()
+                t, calls, threads, host = time_cpu_attention(qn, kf, vf, n, scale, args.cpu_seconds,
+                                                             bits=None)
             extra["cpu_baseline"] = {
-                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "host_cores": host, "blas_threads": 1, "kind": "port",
                 "us_per_call": round(t * 1e6, 1),
-                "sample": f"median of {calls} calls of the oracle's {'dequantize + ' if kind == _lib.LQ_KV_Q4 else ''}"
-                          f"fp32 SDPA at n={n}, one layer, one thread; CPU: {_cpu_model()}"}
+                "sample": f"median of {calls} calls of the oracle's "
+                          f"{'dequantize + ' if kind == _lib.LQ_KV_Q4 else ''}fp32 SDPA at n={n}, "
+                          f"one layer, (KV head, key chunk) tasks on {threads} threads; "
+                          f"CPU: {_cpu_model()}"}
         _result(f"{name} decode-attn GB/s at {n}-token ctx", round(gbs, 2), "GB/s", True, ms, args,
                 "u4" if kind == _lib.LQ_KV_Q4 else "bf16",
                 {"workload": f"{name} KV decode attention, batch 1, {HQ}q/{HKV}kv heads, head_dim {D}, "
@@ -308,21 +351,21 @@ def run_workload(args):
                               "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
                               "kernel": "lq_decode_attn (8-bit, variable-length splits)",
                               "bytes_per_call": nbytes}}
-        if do_cpu:  # one sequence, as the reference would run one call per sequence
-            from oracle import attention as A
-            b0 = 4  # the shortest sequence keeps the sample bounded
-            kh = tuple(t[b0:b0 + 1].cpu() for t in layers[0][0])
-            vh = tuple(t[b0:b0 + 1].cpu() for t in layers[0][1])
+        if do_cpu:  # one call per sequence, as the reference would have to run them
             cv = lambda t: t.numpy() if t.dtype == torch.uint8 else t.view(torch.int16).numpy().view(np.uint16)
-            kh, vh = tuple(map(cv, kh)), tuple(map(cv, vh))
-            qn = q[b0:b0 + 1].float().cpu().numpy()
-            fn = lambda: A.unfused_attention(qn, kh, vh, lens[b0], scale)
-            t, calls = _time_cpu(fn, args.cpu_seconds, min_calls=2)
+            b0 = 4  # the shortest sequence keeps the sample bounded
+            kh = tuple(cv(t[b0].cpu()) for t in layers[0][0])
+            vh = tuple(cv(t[b0].cpu()) for t in layers[0][1])
+            qn = q[b0].float().cpu().numpy()  # [HQ, 1, D]
+            t, calls, threads, host = time_cpu_attention(qn, kh, vh, lens[b0], scale,
+                                                         args.cpu_seconds, min_calls=2)
             extra["cpu_baseline"] = {
-                "value": round(Q8_TOKEN * lens[b0] / t / 1e9, 3), "unit": "GB/s", "cores": 1,
-                "kind": "port", "us_per_call": round(t * 1e6, 1),
-                "sample": f"median of {calls} oracle calls (dequantize + fp64 SDPA) for one sequence of "
-                          f"{lens[b0]} tokens (the reference runs one call per sequence); CPU: {_cpu_model()}"}
+                "value": round(Q8_TOKEN * lens[b0] / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "host_cores": host, "blas_threads": 1, "kind": "port",
+                "us_per_call": round(t * 1e6, 1),
+                "sample": f"median of {calls} calls (dequantize + fp32 SDPA, {threads} threads) for "
+                          f"one sequence of {lens[b0]} tokens (the reference runs one call per "
+                          f"sequence); CPU: {_cpu_model()}"}
         _result("q8 ragged decode-attn GB/s, 8 sequences of 42,771-82,671 tokens", round(gbs, 2),
                 "GB/s", True, ms, args, "u8",
                 {"workload": f"ragged 8-bit decode attention, 8 sequences (sum {sum(lens)} tokens), "
@@ -468,18 +511,19 @@ def run_workload(args):
                                          "lq_q8_verify_append_attn") + " (causal, L=5)",
                               "bytes_per_call": nbytes}}
         if do_cpu:
-            from oracle import attention as A
             cv = lambda t: t.cpu().numpy() if t.dtype == torch.uint8 else t.cpu().view(torch.int16).numpy().view(np.uint16)
-            kh = tuple(cv(t) for t in layers[0][0])
-            vh = tuple(cv(t) for t in layers[0][1])
-            qn = qv.float().cpu().numpy()
-            fn = lambda: A.unfused_attention(qn, kh, vh, nc + L, scale, causal=True)
-            t, calls = _time_cpu(fn, args.cpu_seconds, min_calls=2)
+            kh = tuple(cv(t)[0] for t in layers[0][0])
+            vh = tuple(cv(t)[0] for t in layers[0][1])
+            qn = qv[0].float().cpu().numpy()  # [HQ, L, D]
+            t, calls, threads, host = time_cpu_attention(qn, kh, vh, nc + L, scale,
+                                                         args.cpu_seconds, causal=True,
+                                                         min_calls=2)
             extra["cpu_baseline"] = {
-                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "host_cores": host, "blas_threads": 1, "kind": "port",
                 "us_per_call": round(t * 1e6, 1),
-                "sample": f"median of {calls} oracle calls (dequantize + causal fp64 SDPA) at "
-                          f"{nc + L} keys, L={L}; CPU: {_cpu_model()}"}
+                "sample": f"median of {calls} calls (dequantize + causal fp32 SDPA, {threads} "
+                          f"threads) at {nc + L} keys, L={L}; CPU: {_cpu_model()}"}
         _result("q8 verify-attn (q_len 5, causal) GB/s at 65,541 keys", round(gbs, 2), "GB/s",
                 True, ms, args, "u8",
                 {"workload": f"append 5 rows + causal verify attention, {HQ}q/{HKV}kv heads, "
@@ -658,10 +702,12 @@ def main():
 
     ctx, nl = args.ctx, args.layers
     total_steps = args.warmup + args.steps
-    grow = (total_steps + nl - 1) // nl
-    cap = (ctx + 255) // 256 * 256
-    if ctx + grow > cap:
-        cap += 256
+    # Step i (warm-up steps first) appends at row ctx + i and attends over ctx + i + 1 rows: the
+    # session's consecutive decode steps (n = ctx + 1, ctx + 2, ...), the layer caches rotating
+    # step by step. Every cache holds ctx + total_steps quantized rows, so the rows below each
+    # step's new row are valid whichever layer served the steps before.
+    rows = ctx + total_steps
+    cap = (rows + 255) // 256 * 256
     # ---- caches: N(0,1) bf16 rows quantized on the GPU (group 64, 8-bit)
     layers = []
     for _ in range(nl):
@@ -670,8 +716,8 @@ def main():
             codes = torch.zeros((1, HKV, cap, D), dtype=torch.uint8, device=dev)
             sc = torch.zeros((1, HKV, cap, D // GS), dtype=torch.bfloat16, device=dev)
             bi = torch.zeros_like(sc)
-            x = torch.randn((1, HKV, ctx, D), device=dev, generator=g).to(torch.bfloat16)
-            _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, ctx, D, codes.data_ptr(),
+            x = torch.randn((1, HKV, rows, D), device=dev, generator=g).to(torch.bfloat16)
+            _lib.check(lib.lq_quantize_append(x.data_ptr(), 1, HKV, rows, D, codes.data_ptr(),
                                               sc.data_ptr(), bi.data_ptr(), cap, 0, 8, GS, sp),
                        "prefill quantize")
             del x
@@ -681,7 +727,7 @@ def main():
     ks_new = torch.randn((total_steps, 1, HKV, 1, D), device=dev, generator=g).to(torch.bfloat16)
     vs_new = torch.randn((total_steps, 1, HKV, 1, D), device=dev, generator=g).to(torch.bfloat16)
     out = torch.empty((1, HQ, 1, D), dtype=torch.bfloat16, device=dev)
-    ws_bytes = lib.lq_decode_workspace_bytes(8, 1, HQ, HKV, D, ctx + grow, None)
+    ws_bytes = lib.lq_decode_workspace_bytes(8, 1, HQ, HKV, D, rows, None)
     ws = torch.zeros(ws_bytes * 2, dtype=torch.uint8, device=dev)  # leading counters start at 0
     offsets = [ctx] * nl
     torch.cuda.synchronize()
@@ -711,7 +757,7 @@ def main():
 
     def step(i):
         li = i % nl
-        off = offsets[li]
+        off = ctx + i
         if args.separate_append:
             st = append(i, layers[li], off)
             st |= attend(i, layers[li], off + 1)
@@ -793,9 +839,9 @@ def main():
                                + ("separate append launch" if args.separate_append else "one launch")
                                + "), batch 1, "
                                f"{HQ}q/{HKV}kv heads, head_dim {D}, group {GS}, context {ctx}, "
-                               f"{nl} rotating layer caches",
+                               f"{nl} rotating layer caches; step i attends over ctx + i + 1 rows",
                    "ctx": ctx, "batch": 1, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
-                   "layers": nl, "cap": cap},
+                   "layers": nl, "cap": cap, "n_timed": [ns[0], ns[-1]]},
         "us_per_call": round(total_ms / args.steps * 1e3, 2),
         "attn_us_per_call": ({"mean": round(attn_avg_ms * 1e3, 2), "median": round(attn_med_ms * 1e3, 2)}
                              if attn_ms else None),

@@ -2,8 +2,10 @@
 (``laguna_mlx/laguna.py:75-111``), MI355X side.
 
 ``Attention.__call__`` keeps the reference's protocol: projections, q/k RMSNorm, RoPE at
-``cache.offset``, ``update_and_fetch``, then ``cache.attend`` on fused steps or SDPA over the
-returned K/V otherwise, then the softplus output gate and ``o_proj``. The pieces:
+``cache.offset``, ``update_and_fetch``, then ``cache.attend`` on fused steps, quantized attention
+over the returned packed K/V when the cache exposes ``bits`` (a ``quantized_decode`` step, as
+mlx-lm's SDPA routes it), SDPA over the returned K/V otherwise, then the softplus output gate and
+``o_proj``. The pieces:
 
 * one GEMM for q, k, v and the gate logits (the four projection weights concatenated), one for
   ``o_proj``: ``lq_gemv_bf16`` for a single row (a decode step), hipBLASLt through torch for
@@ -144,6 +146,10 @@ class Attention:
             k, v = cache.update_and_fetch(k, v)
         if getattr(cache, "fused_step", False):
             out = cache.attend(q, self.scale)
+        elif hasattr(cache, "bits"):  # quantized_decode step: packed K/V, quantized attention
+            from .q8_attn import quantized_scaled_dot_product_attention
+            out = quantized_scaled_dot_product_attention(q, k, v, self.scale, mask,
+                                                         cache.group_size, cache.bits)
         else:
             out = _sdpa(q, k, v, mask, self.scale)
         out = out.to(torch.bfloat16).contiguous()

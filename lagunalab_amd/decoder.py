@@ -131,7 +131,7 @@ class DecodeStack:
                             device=dev)
             c.q.reserve(k, k)
             c.q.offset = n0
-        self.n_plan, self.steps_left = n0, steps
+        self.n_plan, self.steps_left, self.next_row = n0, steps, n0
         self.pos = torch.tensor([n0], dtype=torch.int32, device=dev)
         C = self.norms[0].shape[0]
         self.x_in = torch.zeros((1, 1, C), dtype=torch.bfloat16, device=dev)
@@ -143,20 +143,35 @@ class DecodeStack:
             if nb < 0:
                 raise ValueError(lib.lq_last_error().decode())
             self.ws.append(torch.zeros(nb, dtype=torch.uint8, device=dev))  # counters start at 0
+        self.captured_ptrs = self._buffer_ptrs()
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._step_pos()
         torch.cuda.synchronize(dev)
 
+    def _buffer_ptrs(self):
+        return [tuple(t.data_ptr() for t in (*c.q.keys, *c.q.values)) for c in self.caches]
+
     def replay(self, x: torch.Tensor) -> torch.Tensor:
         """Decodes one token with the recorded graph; returns the residual stream out (a view of
-        the graph's output buffer, overwritten by the next replay)."""
+        the graph's output buffer, overwritten by the next replay). Raises if any cache's buffers
+        are not the ones the graph was recorded with (a cache grown by an eager step or an
+        append past the reserved rows, or a reloaded ``state``), or if a cache's offset moved other
+        than by replays (its rows would then not be where the graph's device position appends)."""
         if self.graph is None or self.steps_left <= 0:
             raise RuntimeError("capture() first; the reserved steps are used up")
+        if self._buffer_ptrs() != self.captured_ptrs:
+            # the graph's kernels hold the buffers taken at capture: a cache that grew or was
+            # reloaded since would have its rows written to memory it no longer owns
+            raise RuntimeError("a cache's buffers changed since capture(): capture() again")
+        if any(c._pending is not None or c.q.offset != self.next_row for c in self.caches):
+            # the graph appends at its device position, which only replays advance
+            raise RuntimeError("a cache was appended to or trimmed since capture(): capture() again")
         self.x_in.copy_(x)
         self.graph.replay()
         for c in self.caches:
             c.q.offset += 1
         self.steps_left -= 1
+        self.next_row += 1
         return self.x_out

@@ -19,11 +19,14 @@ from . import _lib
 
 
 class NgramIndex:
-    """Prompt-lookup drafter: g-gram -> most recent start, updated as tokens arrive.
+    """Host-side draft source of the prompt-lookup loop (``laguna_mlx/dflash.py:145-167``).
 
-    ``propose(n)`` equals scanning back for the latest earlier occurrence of the last g tokens and
-    copying up to n tokens after it (never past the current end). Only starts
-    ``s <= len(ids) - g - 1`` are indexed, so the key never matches itself."""
+    ``last`` maps each g-token window of the history to the position where it most recently
+    began; a window enters the map only once at least one token follows it, so the window formed
+    by the newest g tokens is never its own match. ``propose(n)`` looks that newest window up and
+    returns the (at most n) tokens that followed its latest earlier occurrence, cut at the end of
+    the history; ``[]`` when there is none. The result equals a brute-force backward scan, and
+    the device scan ``lq_ngram_propose`` returns the same ids."""
 
     def __init__(self, g):
         self.g, self.ids, self.last = g, [], {}

@@ -37,6 +37,27 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _checked(status: int, what: str, ws: torch.Tensor):
+    """``_lib.check`` for calls that use an attention workspace. A HIP-side failure (a launch that
+    did not start, or a merge launch that failed after the attention kernel ran) can leave the
+    workspace's arrival and tile counters non-zero, and every later call on that stream would then
+    merge too early or skip tiles without an error: the counter area is cleared (on the call's
+    stream, ordered after whatever did run) before the error is raised. Argument errors return
+    before any launch and leave it untouched."""
+    if status == _lib.LQ_EHIP:
+        ws[:_lib.LQ_WS_ZERO_BYTES].zero_()
+    _lib.check(status, what)
+
+
+def reset_workspaces():
+    """Clears the counter area of every cached attention workspace (queued on the streams they
+    belong to). For callers that abandoned a stream's work part way -- an attention launch that
+    was aborted or never completed leaves its counters non-zero."""
+    for (device, stream), ws in _workspaces.items():
+        with torch.cuda.stream(torch.cuda.ExternalStream(stream, device=device)):
+            ws[:_lib.LQ_WS_ZERO_BYTES].zero_()
+
+
 def _as_bytes(codes: torch.Tensor) -> torch.Tensor:
     """Cache codes as a contiguous uint8 tensor [B, H, cap, row_bytes]."""
     if codes.dtype in (torch.int32, torch.uint32):
@@ -136,7 +157,7 @@ def decode_attention(q: torch.Tensor, keys, values, n: int | None = None, scale:
                             vc.data_ptr(), _lib.ptr(vs), _lib.ptr(vb), B, Hq, Hkv, D, cap, int(n),
                             lens_arr, float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
                             _lib.stream_ptr(dev))
-    _lib.check(st, "lq_decode_attn")
+    _checked(st, "lq_decode_attn", ws)
     return out
 
 
@@ -184,7 +205,7 @@ def decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
                                       vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, D, cap, int(n),
                                       lens_arr, float(scale), out.data_ptr(), ws.data_ptr(),
                                       ws.numel(), _lib.stream_ptr(dev))
-    _lib.check(st, "lq_q8_decode_append_attn")
+    _checked(st, "lq_q8_decode_append_attn", ws)
     return out
 
 
@@ -205,6 +226,52 @@ def q8_decode_attention(q, keys, values, n, scale):
         raise AssertionError(f"{G} q heads per kv head is too many for one workgroup")
     out = decode_attention(q.to(torch.bfloat16), keys, values, n=int(n), scale=scale)
     return out.to(q.dtype)
+
+
+def _full_capacity(t: torch.Tensor):
+    """``(buffer, n)`` for a row-prefix view ``t = buf[:, :, :n]`` of a contiguous full-capacity
+    cache buffer ``buf [B, H, cap, w]`` (what ``update_and_fetch`` returns): the buffer is rebuilt
+    as a strided view of the same storage, so the kernels read it in place. Any other layout is
+    copied to a contiguous tensor (then cap = n)."""
+    B, H, n, w = t.shape
+    s0, s1, s2, s3 = t.stride()
+    if s3 == 1 and s2 == w and w > 0 and s1 % w == 0 and s1 // w >= n and s0 == H * s1:
+        cap = s1 // w
+        need = (t.storage_offset() + B * H * cap * w) * t.element_size()
+        if need <= t.untyped_storage().nbytes():
+            return t.as_strided((B, H, cap, w), (s0, s1, s2, 1)), n
+    return t.contiguous(), n
+
+
+def quantized_scaled_dot_product_attention(queries, q_keys, q_values, scale, mask=None,
+                                           group_size=64, bits=8):
+    """Attention over the packed ``(codes, scales, biases)`` views that a ``quantized_decode``
+    step hands the caller -- the routing mlx-lm's SDPA takes when ``hasattr(cache, "bits")``
+    (``laguna_mlx/cache.py:73-77,95-98``; ``docs/interfaces.md:29``). ``q_keys``/``q_values`` are
+    the first ``offset`` rows of the cache buffers; the kernel reads them in place (8- or 4-bit,
+    group 64). Single query rows (the steps on which the cache exposes ``bits``) take the decode
+    kernels; an 8-bit block of up to 16 rows with the bottom-right causal mask takes the verify
+    kernel. Returns ``[B, Hq, L, 128]`` in the queries' dtype."""
+    if group_size != 64:
+        raise ValueError(f"quantized attention takes group_size 64, got {group_size}")
+    B, Hq, L, D = queries.shape
+    kc, n = _full_capacity(q_keys[0])
+    vc, _ = _full_capacity(q_values[0])
+    keys = (kc,) + tuple(_full_capacity(t)[0] for t in q_keys[1:])
+    values = (vc,) + tuple(_full_capacity(t)[0] for t in q_values[1:])
+    row = kc.shape[-1] * (4 if kc.dtype in (torch.int32, torch.uint32) else 1)
+    if row * 8 != D * bits:
+        raise ValueError(f"cache rows of {row} bytes are not {bits}-bit codes of {D} dims")
+    if L == 1:
+        if mask is not None and not isinstance(mask, str):
+            if not bool(torch.as_tensor(mask).all()):
+                raise ValueError("a single query row over the cache takes no mask")
+        out = decode_attention(queries.to(torch.bfloat16), keys, values, n=n, scale=scale)
+        return out.to(queries.dtype)
+    if bits != 8 or L > 16 or mask not in ("causal",):
+        raise ValueError("multi-row quantized attention takes the 8-bit cache, at most 16 rows "
+                         "and the causal mask")
+    return q8_verify_attention(queries, keys, values, n, scale)
 
 
 def q8_verify_attention(q, keys, values, n, scale):
@@ -244,7 +311,7 @@ def q8_verify_attention(q, keys, values, n, scale):
                                vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, L, D, cap,
                                int(n), float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
                                _lib.stream_ptr(dev))
-    _lib.check(st, "lq_q8_verify_attn")
+    _checked(st, "lq_q8_verify_attn", ws)
     return out.to(q.dtype)
 
 
@@ -295,7 +362,7 @@ def q8_verify_append_attention(q, k_new, v_new, keys, values, n, scale):
                                       vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, L, D, cap, int(n),
                                       float(scale), out.data_ptr(), ws.data_ptr(), ws.numel(),
                                       _lib.stream_ptr(dev))
-    _lib.check(st, "lq_q8_verify_append_attn")
+    _checked(st, "lq_q8_verify_append_attn", ws)
     return out.to(q.dtype)
 
 
@@ -388,6 +455,6 @@ def _prefill_blocked(q, keys, values, n, scale):
                                    vc8.data_ptr(), vs.data_ptr(), vb.data_ptr(), B, Hq, Hkv, P, D,
                                    cap, n - L + r + P * (j + 1), float(scale), o0 + j * blk,
                                    ws.data_ptr(), ws.numel(), sp)
-        _lib.check(st, "lq_q8_verify_attn")
+        _checked(st, "lq_q8_verify_attn", ws)
     out[:, :, r:] = ob.permute(1, 2, 0, 3, 4).reshape(B, Hq, L - r, D)
     return out.to(q.dtype)

@@ -431,3 +431,50 @@ def test_graph_step_matches_eager(dev):
             assert torch.equal(x, y)
     with pytest.raises(RuntimeError, match="used up"):
         b.replay(x)
+
+
+def test_graph_replay_refuses_changed_caches(dev):
+    """A replay after a cache's buffers moved (an eager step past the reserved rows regrows them)
+    or after its offset moved outside the replays raises instead of writing freed memory."""
+    s = _stack(dev, 43, 1000)
+    s.capture(steps=2)
+    rng = np.random.default_rng(44)
+    s.replay(_bf16(rng, (1, 1, 512)))
+    s.caches[0].q.offset += 1  # an append the graph does not know about
+    with pytest.raises(RuntimeError, match="appended to or trimmed"):
+        s.replay(_bf16(rng, (1, 1, 512)))
+    s.caches[0].q.offset -= 1
+    c = s.caches[1]
+    k = torch.zeros((1, c.q.keys[0].shape[1], 300, 128), dtype=torch.bfloat16, device=dev)
+    c.q.reserve(k, k)  # grows past the capacity reserved at capture: new buffers
+    c.q.offset -= 300
+    with pytest.raises(RuntimeError, match="buffers changed"):
+        s.replay(_bf16(rng, (1, 1, 512)))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_attention_block_quantized_decode_routes_packed_kv(dev, bits):
+    """``quantized_decode``: on single-token steps the cache returns the packed (codes, scales,
+    biases) views and exposes ``bits``; the block routes them to the quantized decode kernels (as
+    mlx-lm's SDPA routes them on ``hasattr(cache, "bits")``). Against the dequantizing cache's
+    block output: within the fused-vs-unfused attention difference carried through the gate and
+    o_proj."""
+    from lagunalab_amd.attention import Attention
+    from lagunalab_amd.cache import DequantKVCache
+    rng = np.random.default_rng(12 + bits)
+    C, H, Hkv, D = 512, 8, 2, 128
+    rope = {"rope_theta": 1e4}
+    w = lambda *s: _bf16(rng, s, 0.05)
+    blk = Attention(w(H * D, C), w(Hkv * D, C), w(Hkv * D, C), w(C, H * D), w(H, C),
+                    _bf16(rng, (D,), 0.1) + 1, _bf16(rng, (D,), 0.1) + 1, H, Hkv, rope)
+    qd, plain = DequantKVCache(bits=bits, quantized_decode=True), DequantKVCache(bits=bits)
+    for L in (700, 1, 1, 3, 1):
+        x = _bf16(rng, (1, L, C))
+        a = blk(x, qd.make_mask(L), qd)
+        assert hasattr(qd, "bits") == (L == 1)
+        want = blk(x, plain.make_mask(L), plain)
+        err = float((a.float() - want.float()).abs().max())
+        scale = float(want.float().abs().max())
+        assert err <= 2e-2 * scale, (L, err, scale)
+        if L > 1:
+            assert torch.equal(a, want)  # multi-row steps take the dequantize path in both

@@ -78,6 +78,31 @@ def test_fused_greedy_tokens_equal_unfused(model):
     assert got == want
 
 
+@torch.no_grad()
+def test_quantized_decode_greedy_tokens_equal_dequantize_path(model):
+    """``make_quantized_cache(model, 8, quantized_decode=True)``: single-token steps hand the model
+    the packed K/V and expose ``bits``; the model routes them to the quantized decode kernel (the
+    reference's switch, ``laguna_mlx/cache.py:73-77,95-98``). Same greedy tokens as the default
+    dequantize path."""
+    want = _greedy(model, PROMPT, 40, lambda: make_quantized_cache(model, 8))
+    got = _greedy(model, PROMPT, 40, lambda: make_quantized_cache(model, 8, quantized_decode=True))
+    assert got == want
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantized_decode_logits_match_dequantize_path(model, bits):
+    ids = torch.tensor([[5, 9, 2, 7, 1, 3, 8, 4] * 40], device="cuda")
+    out = []
+    for qd in (False, True):
+        cache = make_quantized_cache(model, bits, quantized_decode=qd)
+        model(ids, cache=cache)
+        tok = torch.tensor([[6]], device="cuda")
+        out.append(torch.cat([model(tok, cache=cache) for _ in range(3)], dim=1))
+    assert (out[0] - out[1]).abs().max().item() < 5e-2 * out[0].abs().max().item()
+    assert torch.equal(out[0].argmax(-1), out[1].argmax(-1))
+
+
 def _echo_prompt(model):
     # The random model rarely repeats itself; a prompt that echoes its own prefix gives natural
     # lookup hits at g=2.

@@ -1,6 +1,7 @@
 """Tiny random decoder for the generation tests: the attention protocol of
 ``laguna_mlx/laguna.py:94-111`` (q/k RMSNorm, RoPE at ``cache.offset``, ``update_and_fetch``,
-``fused_step`` -> ``cache.attend``, else SDPA with the cache's mask, per-head softplus gate),
+``fused_step`` -> ``cache.attend``, ``bits`` -> quantized attention over the packed K/V, else SDPA
+with the cache's mask, per-head softplus gate),
 full-attention and sliding-window layers, head_dim 128 so that the HIP decode and verify kernels
 take the full-attention layers. Weights and the residual stream are float32; the attention
 operands (q, k, v after RoPE) and its output are rounded to ``attn_dtype`` (bf16 by default, what
@@ -122,6 +123,10 @@ class TinyLM(torch.nn.Module):
         scale = 1.0 / math.sqrt(D)
         if getattr(cache, "fused_step", False):
             out = cache.attend(q, scale)
+        elif hasattr(cache, "bits"):  # quantized_decode step: packed K/V (mlx-lm's SDPA routing)
+            from lagunalab_amd.q8_attn import quantized_scaled_dot_product_attention
+            out = quantized_scaled_dot_product_attention(q, k, v, scale, mask, cache.group_size,
+                                                         cache.bits)
         else:
             out = sdpa(q, k, v, mask, scale)
         out = out.to(x.dtype).transpose(1, 2)  # B, L, H, D
