@@ -37,6 +37,7 @@ struct Bf16Smem {
     alignas(16) float acc[BW][4][D];
   };
   alignas(16) float st[BW][4][6];
+  alignas(16) uint8_t qstage[BW][4 * D * 2];  // each wave's copy of the (<= 4) q rows
 };
 
 __device__ __forceinline__ bf16x8_t u4_as_bf8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
@@ -218,30 +219,48 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
 
   const std::integral_constant<int, 0> B0;
   const std::integral_constant<int, 1> B1;
-  issue(0, B0);
+  // Prologue: the R q rows (contiguous, <= 1 KB) by DMA into this wave's staging area, then
+  // super-tile 0; only the q copy is waited for before the q operands are built. Nothing is
+  // issued for super-tiles past the wave's range.
+  {
+    const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;
+    dma_b128<0>(qblk, (uint32_t)min(16 * lane, R * 2 * D - 16), lds_addr(&sm.qstage[wv][0]));
+  }
+  if (nst > 0) issue(0, B0);
+  if (nst > 0)
+    asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // q as block-diagonal bf16 B operands: q[rho] dims 8 s .. 8 s + 7 when lane group lq4 == mt
   {
     const bool on = qvalid && mt == lq4;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
+    const uint8_t* qr = &sm.qstage[wv][0] + (gh * L + qi) * 2 * D;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * s);
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * s);
       qb[s] = u4_as_bf8(on ? u : make_uint4(0u, 0u, 0u, 0u));
     }
   }
 
+  // Step si issues super-tile si + 1 (if in range), waits for si (all but the copies of si + 1),
+  // processes it.
   for (int si = 0; si < nst; si += 2) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    issue(si + 1, B1);
-    asm volatile("s_waitcnt vmcnt(32)" ::: "memory");  // super-tile si has landed in LDS
-    process(si, B0);
-    if (si + 1 < nst) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(si + 2, B0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer refilled next are done
+    if (si + 1 < nst) issue(si + 1, B1);
+    if (si + 1 < nst)
       asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-      process(si + 1, B1);
-    }
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    process(si, B0);
+    if (si + 1 >= nst) break;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (si + 2 < nst) issue(si + 2, B0);
+    if (si + 2 < nst)
+      asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    process(si + 1, B1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below

@@ -19,7 +19,7 @@
 //    query row; softmax runs in that layout (row max: in-lane over mt and r, then over the 4
 //    lane groups), with lazy rescaling and exp2 of scores pre-scaled by scale * log2(e).
 //  * P.V: two k-steps of 32 keys (M tiles 2e and 2e+1); A = V^T (16 dims x 32 keys) from one
-//    transposed 8-byte LDS read (ds_read_b64_tr_b8), B = P * V scale in fp16 built from the
+//    transposed 8-byte LDS read (ds_read_b64_tr_b8), B = P * V scale * 2^kv in fp16 built from the
 //    lane's own weights (k-slot j of lane group q = key 16 (2e + j / 4) + 4 q + j % 4).
 //  * Work: the waves of a sequence's workgroups take super-tiles gw, gw + NWS, ... (static,
 //    interleaved); K, V and the word arrays of a super-tile go global -> LDS with 20 DMA copies,
@@ -266,22 +266,37 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
     }
   };
 
-  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+  // Per-key K factor: scale * log2(e) * 2^24 (codes enter the MFMA as c * 2^-24) / 2^kq (the q
+  // operands' power-of-two factor, set with them below).
+  float kscale = qk_scale_log2 * 16777216.0f;
+  VScale vsc;  // P.V factors 2^kv of the two quant groups (set by the first tile)
 
   auto process = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * DST;
     const DenseBuf& pb = sm.loop.buf[wv][BUF];
-    if (ST == 64 || lane < ST) {  // per-key terms, one lane per key
-      const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
-      tm.ks0[lane] = bf16_lo(a) * kscale;
-      tm.ks1[lane] = bf16_hi(a) * kscale;
-      tm.ku0[lane] = bf16_lo(c);
-      tm.ku1[lane] = bf16_hi(c);
-      tm.vs0[lane] = bf16_lo(e);
-      tm.vs1[lane] = bf16_hi(e);
-      tm.vb0[lane] = bf16_lo(f);
-      tm.vb1[lane] = bf16_hi(f);
+    // per-key terms, one lane per key (V scales scaled by the wave's P.V factors; |scale_v| of
+    // valid keys kept for their check)
+    const bool kl = ST == 64 || lane < ST;
+    float sv0, sv1, va0, va1;
+    {
+      const int kk = kl ? lane : 0;
+      const uint32_t a = pb.ks[kk], c = pb.kb[kk], e = pb.vs[kk], f = pb.vb[kk];
+      sv0 = bf16_lo(e);
+      sv1 = bf16_hi(e);
+      const bool kv = kl && t0 + lane < n;  // rows past n are clamped copies, never attended
+      va0 = kv ? fabsf(sv0) : 0.0f;
+      va1 = kv ? fabsf(sv1) : 0.0f;
+      if (kl) {
+        tm.ks0[lane] = bf16_lo(a) * kscale;
+        tm.ks1[lane] = bf16_hi(a) * kscale;
+        tm.ku0[lane] = bf16_lo(c);
+        tm.ku1[lane] = bf16_hi(c);
+        tm.vs0[lane] = sv0 * vsc.f0;
+        tm.vs1[lane] = sv1 * vsc.f1;
+        tm.vb0[lane] = bf16_lo(f);
+        tm.vb1[lane] = bf16_hi(f);
+      }
     }
     // Q.K^T: c[mt][nt][g]
     f4_t c[MT][NT][2];
@@ -306,6 +321,7 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool vnew = vscale_check(va0, va1, vsc);  // new P.V factors: applied with N tile 0
     const bool full = t0 + DST <= n && (!CAUSAL || t0 + DST - 1 <= causal_base);
     // scores of this lane's keys 16 mt + 4 lq4 + r, per N tile (per-key terms read per M tile)
     float sc[NT][MT][4];
@@ -345,15 +361,29 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
       tmax = max_xor16(tmax);
       tmax = max_xor32(tmax);
       const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
-      if (__builtin_amdgcn_ballot_w64(bump)) {
-        const float mn = bump ? tmax : m_run[nt];
-        const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
-        m_run[nt] = mn;
-        lsum[nt] *= alpha;
-        bsum[nt][0] *= alpha;
-        bsum[nt][1] *= alpha;
+      const uint64_t bumps = __builtin_amdgcn_ballot_w64(bump);
+      const bool vn = nt == 0 && vnew;
+      if (bumps || vn) {  // rare: a new running max, or new P.V factors
+        if (bumps) {
+          const float mn = bump ? tmax : m_run[nt];
+          const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
+          m_run[nt] = mn;
+          lsum[nt] *= alpha;
+          bsum[nt][0] *= alpha;
+          bsum[nt][1] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+          for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+        }
+        if (vn) {  // every N tile's accumulators; the V terms read below are rewritten
+          vscale_apply<NT>(va0, va1, vsc, &oacc[0][0]);
+          if (kl) {
+            tm.vs0[lane] = sv0 * vsc.f0;
+            tm.vs1[lane] = sv1 * vsc.f1;
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
       }
       const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float ls = 0.f, b0 = 0.f, b1 = 0.f;
@@ -419,10 +449,22 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
   const std::integral_constant<int, 0> B0;
   const std::integral_constant<int, 1> B1;
   // Unrolled by two so that each buffer's LDS offsets are constants. The next super-tile is
-  // always issued before the current one is processed (past the end the copies clamp to the last
-  // row and are never read), so the wait is a fixed count: the 20 copies issued after it.
+  // issued before the current one is processed, so the wait is a fixed count (the copies issued
+  // after it), except at the end, where nothing past the last super-tile is issued.
   int cur = min(gw, T);
-  issue(cur, B0);  // the first super-tile streams in while q and the new rows are loaded
+  // Prologue: the R q rows (contiguous, R * 256 <= 16 KB) go by DMA into this wave's second
+  // buffer, free until super-tile 1 is issued; then the staging waves' new rows (plain loads)
+  // and super-tile 0. Only the q copies and the new rows are waited for before the q operands
+  // are built; super-tile 0 streams in meanwhile.
+  {
+    const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;
+    const int qbytes = R * 2 * D;
+    const uint32_t qlds = lds_bufs + (uint32_t)sizeof(DenseBuf);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (1024 * i < qbytes)  // wave-uniform
+        dma_b128<0>(qblk, (uint32_t)min(1024 * i + 16 * lane, qbytes - 16), qlds + 1024 * i);
+  }
   // staging wave: the new rows sr0 + si + nstage i (at most 8 with L <= 16), loads issued
   // together with q's
   uint32_t kraw[8], vraw[8];
@@ -434,36 +476,62 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
     kraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.knew + src) : 0u;
     vraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.vnew + src) : 0u;
   }
+  if (cur < T) issue(cur, B0);
+  if (cur < T) {  // the q copies and the new rows have landed
+    if constexpr (NCOPY == 20)
+      asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 
+  // q operands: one power-of-two factor for all rows of the wave (the largest |q| element of any
+  // row in [2^14, 2^15) before the fp16 conversion); 2^-kq goes into kscale
+  {
+    uint32_t qwd[NT][2][8];
+    uint32_t mbits = 0u;
+    const uint8_t* qstage = reinterpret_cast<const uint8_t*>(&sm.loop.buf[wv][1]);
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int qr_i = 16 * nt + lc;
-    const bool valid = qr_i < R;
-    const int gh = valid ? qr_i / L : 0;
-    const int i = valid ? qr_i - gh * L : 0;
-    qpos[nt] = i;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + i) * D;
+    for (int nt = 0; nt < NT; ++nt) {
+      const int qr_i = 16 * nt + lc;
+      const bool valid = qr_i < R;
+      const int gh = valid ? qr_i / L : 0;
+      const int i = valid ? qr_i - gh * L : 0;
+      qpos[nt] = i;
+      const uint8_t* qr = qstage + (gh * L + i) * 2 * D;  // row gh * L + i of the block
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float s = 0.0f;
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4);
-      const uint4 v = *reinterpret_cast<const uint4*>(qr + 64 * g + 16 * lq4 + 8);
-      const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+      for (int g = 0; g < 2; ++g) {
+        const uint4 u = *reinterpret_cast<const uint4*>(qr + 2 * (64 * g + 16 * lq4));
+        const uint4 v = *reinterpret_cast<const uint4*>(qr + 2 * (64 * g + 16 * lq4 + 8));
+        const uint32_t w[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        float s = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t wd = w[4 * e + j];
-          const _Float16 lo = valid ? (_Float16)bf16_lo(wd) : (_Float16)0.0f;
-          const _Float16 hi = valid ? (_Float16)bf16_hi(wd) : (_Float16)0.0f;
-          qb[nt][g][e][2 * j] = lo;
-          qb[nt][g][e][2 * j + 1] = hi;
-          s += (float)lo + (float)hi;
+        for (int j = 0; j < 8; ++j) {
+          qwd[nt][g][j] = valid ? w[j] : 0u;
+          mbits = bf16x2_absmax_bits(mbits, qwd[nt][g][j]);
+          s += bf16_lo(qwd[nt][g][j]) + bf16_hi(qwd[nt][g][j]);
         }
-      s += shfl_xor_f(s, 16);
-      s += shfl_xor_f(s, 32);
-      qsum[nt][g] = s * qk_scale_log2;
+        s += shfl_xor_f(s, 16);
+        s += shfl_xor_f(s, 32);
+        qsum[nt][g] = s * qk_scale_log2;
+      }
     }
+    const int kq = q_pow2_exp(bf16x2_max_value(mbits));
+    const float qf = pow2f(kq);
+    kscale = qk_scale_log2 * pow2f(24 - kq);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t wd = qwd[nt][g][4 * e + j];
+            qb[nt][g][e][2 * j] = (_Float16)(bf16_lo(wd) * qf);
+            qb[nt][g][e][2 * j + 1] = (_Float16)(bf16_hi(wd) * qf);
+          }
   }
 
   if (stager) {
@@ -496,9 +564,13 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
     if (lane == 0)
       __hip_atomic_fetch_add(&sm.stg.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  // Waits until only the NCOPY copies of the super-tile issued last are outstanding.
-  auto wait_tile = [&]() {
-    if constexpr (NCOPY == 20)
+  // Waits for the super-tile in process order: until only the NCOPY copies of the super-tile
+  // issued after it are outstanding, or until nothing is when that one was past the end (not
+  // issued).
+  auto wait_tile = [&](bool next_issued) {
+    if (!next_issued)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (NCOPY == 20)
       asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
@@ -516,26 +588,29 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
   for (;;) {
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer reused next are done
-    issue(min(cur + NWS, T), B1);
-    wait_tile();  // super-tile cur has landed in LDS
+    int nx = min(cur + NWS, T);
+    if (nx < T) issue(nx, B1);
+    wait_tile(nx < T);  // super-tile cur has landed in LDS
     if (app && (cur == ta || cur == tb)) {
       staged();
       patch(cur, B0);
     }
     process(cur, B0);
-    cur = min(cur + NWS, T);
+    cur = nx;
     if (cur >= T) break;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    issue(min(cur + NWS, T), B0);
-    wait_tile();
+    nx = min(cur + NWS, T);
+    if (nx < T) issue(nx, B0);
+    wait_tile(nx < T);
     if (app && (cur == ta || cur == tb)) {
       staged();
       patch(cur, B1);
     }
     process(cur, B1);
-    cur = min(cur + NWS, T);
+    cur = nx;
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vscale_remove<NT>(vsc, &oacc[0][0]);
 
   // ---- per-wave totals over the 4 lane groups that share a column
 #pragma unroll

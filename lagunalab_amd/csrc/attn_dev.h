@@ -46,6 +46,107 @@ __device__ __forceinline__ uint32_t pack_h2(float x, float y) {
 
 __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
 
+// ---- fp16 operand range. The MFMA operands are fp16 (normal from 2^-14 to 65504, subnormal
+// steps of 2^-24), while the reference computes in fp32 (q8_attn.py:117). Two power-of-two
+// factors keep the operands where fp16 holds them to 11 bits, and come back out exactly:
+//  * q: every query row of a wave is multiplied by one 2^kq that puts the largest |q| element in
+//    [2^14, 2^15) before the fp16 conversion (exact for bf16 values in the normal range); 2^-kq
+//    goes into the per-key K factor. Supported: finite q with max |q| in about [1e-25, 1e34];
+//    elements more than 2^28 below a wave's largest lose bits, at a relative weight < 2^-28.
+//  * P.V: B = p * scale_v * 2^kv per quant group and wave, 2^kv chosen so that the largest
+//    |scale_v| of the valid keys of a super-tile lies in [16, 32); it is kept while that largest
+//    value stays within [0.25, 128] (p <= 2^8 under the lazy softmax rescale, so B <= 2^15), and
+//    otherwise re-chosen and the group's accumulators rescaled by the exact ratio. 2^-kv is taken
+//    out before the epilogue. Supported: |scale_v| in about [3e-11, 1.7e13] (kv in [-40, 40]).
+
+// 2^k as a float, k in [-126, 127].
+__device__ __forceinline__ float pow2f(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+
+// k with amax * 2^k in [2^(e - 1), 2^e), clamped to [lo, hi]; amax > 0 and finite.
+__device__ __forceinline__ int pow2_exp_into(float amax, int e, int lo, int hi) {
+  return min(max(e - __builtin_amdgcn_frexp_expf(amax), lo), hi);
+}
+
+// Max over all 64 lanes on the VALU (DPP row steps, then row and half swaps); all lanes active.
+__device__ __forceinline__ float wave_max_valu(float x) {
+  x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_ROW_ROR4>(x));
+  x = fmaxf(x, dpp<DPP_ROW_ROR8>(x));
+  return max_xor32(max_xor16(x));
+}
+
+// Largest magnitude of the two bf16 values of a dword, as bf16 bits (an unsigned 16-bit max of
+// the magnitudes orders them like the values; NaN payloads compare above infinity).
+__device__ __forceinline__ uint32_t bf16x2_absmax_bits(uint32_t acc, uint32_t w) {
+  typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+  const u16x2_t a = __builtin_bit_cast(u16x2_t, acc), b = __builtin_bit_cast(u16x2_t, w & 0x7fff7fffu);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+__device__ __forceinline__ float bf16x2_max_value(uint32_t m) {
+  return fmaxf(bf16_lo(m), bf16_hi(m));
+}
+
+// The q exponent kq of a wave from the largest |q| element any lane of it holds (0 when q is 0).
+__device__ __forceinline__ int q_pow2_exp(float amax_lane) {
+  const float m = wave_max_valu(amax_lane);
+  return m > 0.0f ? pow2_exp_into(m, 15, -100, 100) : 0;
+}
+
+constexpr float VF_HI = 128.0f;  // re-choose the P.V factor when a scaled |scale_v| exceeds this
+constexpr float VF_LO = 0.25f;   // ... or when all of a super-tile's are below this
+constexpr int VK_NONE = -1000;   // P.V exponent before the first key with a nonzero V scale
+
+// The P.V exponents kv of a wave, one per quant group, and their factors 2^kv (0 before set).
+struct VScale {
+  int k0 = VK_NONE, k1 = VK_NONE;
+  float f0 = 0.0f, f1 = 0.0f;
+};
+
+// Whether the P.V factors of a wave must be re-chosen for the super-tile whose keys the lanes
+// hold: a0 / a1 are |scale_v| of this lane's key (0 for keys past the sequence). All 64 lanes
+// active; every lane passes its key's values; the result is wave-uniform. Kernels test it in the
+// same branch as the lazy softmax rescale, so the hot path gets no branch of its own.
+__device__ __forceinline__ bool vscale_check(float a0, float a1, const VScale& v) {
+  const bool over = fmaxf(a0 * v.f0, a1 * v.f1) > VF_HI;
+  const uint64_t big0 = __builtin_amdgcn_ballot_w64(a0 * v.f0 >= VF_LO);
+  const uint64_t big1 = __builtin_amdgcn_ballot_w64(a1 * v.f1 >= VF_LO);
+  return (__builtin_amdgcn_ballot_w64(over) | (big0 == 0) | (big1 == 0)) != 0;
+}
+
+// Re-chooses the P.V factors (after vscale_check returned true) and rescales the accumulators by
+// the exact ratio. oacc: NACC sets of 8 accumulators, in each of which [0..3] hold group 0 dims
+// and [4..7] group 1 (in every kernel that calls this). The caller then rewrites the scaled V
+// terms of the tile.
+template <int NACC = 1>
+__device__ __forceinline__ void vscale_apply(float a0, float a1, VScale& v, f4_t* oacc) {
+  const float m0 = wave_max_valu(a0), m1 = wave_max_valu(a1);
+  const int n0 = m0 > 0.0f ? pow2_exp_into(m0, 5, -40, 40) : v.k0;
+  const int n1 = m1 > 0.0f ? pow2_exp_into(m1, 5, -40, 40) : v.k1;
+  // exact power-of-two ratios; an unset factor (0) had produced zero accumulators
+  const float r0 = v.k0 == VK_NONE ? 0.0f : pow2f(n0 - v.k0);
+  const float r1 = v.k1 == VK_NONE ? 0.0f : pow2f(n1 - v.k1);
+#pragma unroll
+  for (int i = 0; i < NACC; ++i)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[8 * i + dt] *= dt < 4 ? r0 : r1;
+  v.k0 = n0;
+  v.k1 = n1;
+  v.f0 = n0 == VK_NONE ? 0.0f : pow2f(n0);
+  v.f1 = n1 == VK_NONE ? 0.0f : pow2f(n1);
+}
+
+// Takes the P.V factors back out of the accumulators (before the epilogue).
+template <int NACC = 1>
+__device__ __forceinline__ void vscale_remove(const VScale& v, f4_t* oacc) {
+  const float i0 = v.k0 == VK_NONE ? 1.0f : pow2f(-v.k0);
+  const float i1 = v.k1 == VK_NONE ? 1.0f : pow2f(-v.k1);
+#pragma unroll
+  for (int i = 0; i < NACC; ++i)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[8 * i + dt] *= dt < 4 ? i0 : i1;
+}
+
 // Global -> LDS copies (LDS destination = lds_base + size * lane; lds_base wave-uniform). They are
 // issued as inline asm on purpose: the compiler then has no pending LDS write to guard and adds no
 // blanket vmcnt(0) in front of every LDS read, which would wait for the prefetched tile too.

@@ -166,20 +166,29 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
 
   const uint32_t sel_lo0 = mt == 0 ? ~0u : 0u, sel_hi0 = mt == 1 ? ~0u : 0u;
   const uint32_t sel_lo1 = mt == 2 ? ~0u : 0u, sel_hi1 = mt == 3 ? ~0u : 0u;
-  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+  // Per-key K factor: scale * log2(e) * 2^24 (codes enter the MFMA as c * 2^-24) / 2^kq (the q
+  // operands' power-of-two factor, set with them below).
+  float kscale = qk_scale_log2 * 16777216.0f;
+  VScale vsc;  // P.V factors 2^kv of the two quant groups (set by the first tile)
 
   auto process = [&](int si, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = w_begin + si * QPST;
     const Q4Buf& pb = sm.loop.buf[wv][BUF];
+    float sv0, sv1, va0, va1;  // V scales of this lane's key; |scale_v| if valid
     {
       const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
+      sv0 = bf16_lo(e);
+      sv1 = bf16_hi(e);
+      const bool kv = t0 + lane < w_end;  // rows past the wave's range are clamped copies
+      va0 = kv ? fabsf(sv0) : 0.0f;
+      va1 = kv ? fabsf(sv1) : 0.0f;
       tm.ks0[lane] = bf16_lo(a) * kscale;
       tm.ks1[lane] = bf16_hi(a) * kscale;
       tm.ku0[lane] = bf16_lo(c);
       tm.ku1[lane] = bf16_hi(c);
-      tm.vs0[lane] = bf16_lo(e);
-      tm.vs1[lane] = bf16_hi(e);
+      tm.vs0[lane] = sv0 * vsc.f0;
+      tm.vs1[lane] = sv1 * vsc.f1;
       tm.vb0[lane] = bf16_lo(f);
       tm.vb1[lane] = bf16_hi(f);
     }
@@ -232,15 +241,27 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;
-    if (__builtin_amdgcn_ballot_w64(bump)) {
-      const float mn = bump ? tmax : m_run;
-      const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
-      m_run = mn;
-      lsum *= alpha;
-      bsum0 *= alpha;
-      bsum1 *= alpha;
+    const uint64_t bumps = __builtin_amdgcn_ballot_w64(bump);
+    const bool vnew = vscale_check(va0, va1, vsc);
+    if (bumps || vnew) {  // rare: a new running max, or new P.V factors
+      if (bumps) {
+        const float mn = bump ? tmax : m_run;
+        const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
+        m_run = mn;
+        lsum *= alpha;
+        bsum0 *= alpha;
+        bsum1 *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+      }
+      if (vnew) {  // the terms read below are rewritten with the new factors
+        vscale_apply(va0, va1, vsc, oacc);
+        tm.vs0[lane] = sv0 * vsc.f0;
+        tm.vs1[lane] = sv1 * vsc.f1;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
     }
     const float mref = m_run == -INFINITY ? 0.0f : m_run;
     const float4 vs0 = *reinterpret_cast<const float4*>(tm.vs0 + k0);
@@ -287,42 +308,77 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
 
   const std::integral_constant<int, 0> B0;
   const std::integral_constant<int, 1> B1;
-  issue(0, B0);
-
+  // Prologue: the R q rows (contiguous, <= 1 KB) go to this wave's terms area by DMA (free until
+  // the first super-tile is processed), then super-tiles 0 and 1; only the q copy is waited for
+  // before the q operands are built, so both super-tiles stream in meanwhile. Nothing is issued
+  // for super-tiles past the wave's range.
   {
+    const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;
+    dma_b128<0>(qblk, (uint32_t)min(16 * lane, R * 2 * D - 16), lds_addr(&tm));
+  }
+  if (nst > 0) issue(0, B0);
+  if (nst > 1) issue(1, B1);
+  if (nst > 1)
+    asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (nst > 0)
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  {  // q operands times the wave's power-of-two q factor (every lane reads a whole row)
     const bool on = qvalid && mt == lq4;
-    const uint16_t* qr = q + (((int64_t)b * Hq + hk * G + gh) * L + qi) * D;
-    float sg[2] = {0.f, 0.f};
+    const uint8_t* qr = reinterpret_cast<const uint8_t*>(&tm) + (gh * L + qi) * 2 * D;
+    uint32_t w[64];
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 8 * st);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * st);
+      w[4 * st] = u.x;
+      w[4 * st + 1] = u.y;
+      w[4 * st + 2] = u.z;
+      w[4 * st + 3] = u.w;
+    }
+    uint32_t mbits = 0u;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const _Float16 lo = (_Float16)bf16_to_f32((uint16_t)(w[j] & 0xffffu));
-        const _Float16 hi = (_Float16)bf16_to_f32((uint16_t)(w[j] >> 16));
-        qb[st][2 * j] = on ? lo : (_Float16)0.0f;
-        qb[st][2 * j + 1] = on ? hi : (_Float16)0.0f;
-        sg[st >> 3] += (float)lo + (float)hi;
-      }
+    for (int i = 0; i < 64; ++i) mbits = bf16x2_absmax_bits(mbits, w[i]);
+    const int kq = q_pow2_exp(qvalid ? bf16x2_max_value(mbits) : 0.0f);
+    const float qf = pow2f(kq);
+    kscale = qk_scale_log2 * pow2f(24 - kq);
+    float sg[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const float lo = bf16_lo(w[i]), hi = bf16_hi(w[i]);
+      sg[i >> 5] += lo + hi;
+      qb[i >> 2][2 * (i & 3)] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
+      qb[i >> 2][2 * (i & 3) + 1] = on ? (_Float16)(hi * qf) : (_Float16)0.0f;
     }
     qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
     qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // q reads done before terms overwrite
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+  // Step si waits for super-tile si (all but the copies of si + 1, when those were issued),
+  // processes it, then refills its buffer with super-tile si + 2 if that is in range.
   for (int si = 0; si < nst; si += 2) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    issue(si + 1, B1);
-    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // super-tile si has landed in LDS
-    process(si, B0);
-    if (si + 1 < nst) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(si + 2, B0);
+    if (si + 1 < nst)
       asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      process(si + 1, B1);
-    }
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    process(si, B0);
+    if (si + 1 >= nst) break;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer refilled next are done
+    if (si + 2 < nst) issue(si + 2, B0);
+    if (si + 2 < nst)
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    process(si + 1, B1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (si + 3 < nst) issue(si + 3, B1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vscale_remove(vsc, oacc);
   __syncthreads();
   packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.fin.acc[0][0][0],
                           &sm.fin.st[0][0][0], &sm.fin.last, args, plan, x, b, hk, R);

@@ -204,21 +204,31 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   // slots 4-7): this lane's own key tile is mt.
   const uint32_t sel_lo0 = mt == 0 ? ~0u : 0u, sel_hi0 = mt == 1 ? ~0u : 0u;
   const uint32_t sel_lo1 = mt == 2 ? ~0u : 0u, sel_hi1 = mt == 3 ? ~0u : 0u;
-  const float kscale = qk_scale_log2 * 16777216.0f;  // 2^24: codes enter the MFMA as c * 2^-24
+  // Per-key K factor: scale * log2(e) * 2^24 (codes enter the MFMA as c * 2^-24) / 2^kq (the q
+  // operands' power-of-two factor, set with them below).
+  float kscale = qk_scale_log2 * 16777216.0f;
+  VScale vsc;  // P.V factors 2^kv of the two quant groups (set by the first tile)
 
   auto process = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * PST;
     const PackBuf& pb = sm.loop.buf[wv][BUF];
     // per-key terms, one lane per key: K scale * scale * log2(e) * 2^24, K bias, V scale, V bias
+    // (V scales scaled by the wave's P.V factors; |scale_v| of valid keys kept for their check)
+    float sv0, sv1, va0, va1;
     {
       const uint32_t a = pb.ks[lane], c = pb.kb[lane], e = pb.vs[lane], f = pb.vb[lane];
+      sv0 = bf16_lo(e);
+      sv1 = bf16_hi(e);
+      const bool kv = t0 + lane < n;  // rows past n are clamped copies, never attended
+      va0 = kv ? fabsf(sv0) : 0.0f;
+      va1 = kv ? fabsf(sv1) : 0.0f;
       tm.ks0[lane] = bf16_lo(a) * kscale;
       tm.ks1[lane] = bf16_hi(a) * kscale;
       tm.ku0[lane] = bf16_lo(c);
       tm.ku1[lane] = bf16_hi(c);
-      tm.vs0[lane] = bf16_lo(e);
-      tm.vs1[lane] = bf16_hi(e);
+      tm.vs0[lane] = sv0 * vsc.f0;
+      tm.vs1[lane] = sv1 * vsc.f1;
       tm.vb0[lane] = bf16_lo(f);
       tm.vb1[lane] = bf16_hi(f);
     }
@@ -270,15 +280,27 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;
-    if (__builtin_amdgcn_ballot_w64(bump)) {
-      const float mn = bump ? tmax : m_run;
-      const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
-      m_run = mn;
-      lsum *= alpha;
-      bsum0 *= alpha;
-      bsum1 *= alpha;
+    const uint64_t bumps = __builtin_amdgcn_ballot_w64(bump);
+    const bool vnew = vscale_check(va0, va1, vsc);
+    if (bumps || vnew) {  // rare: a new running max, or new P.V factors
+      if (bumps) {
+        const float mn = bump ? tmax : m_run;
+        const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
+        m_run = mn;
+        lsum *= alpha;
+        bsum0 *= alpha;
+        bsum1 *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+      }
+      if (vnew) {  // the terms read below are rewritten with the new factors
+        vscale_apply(va0, va1, vsc, oacc);
+        tm.vs0[lane] = sv0 * vsc.f0;
+        tm.vs1[lane] = sv1 * vsc.f1;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
     }
     const float mref = m_run == -INFINITY ? 0.0f : m_run;
     const float4 vs0 = *reinterpret_cast<const float4*>(tm.vs0 + k0);
@@ -295,7 +317,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
       bsum0 = fmaf(p[r], vb0v[r], bsum0);
       bsum1 = fmaf(p[r], vb1v[r], bsum1);
     }
-    // P * scale_v in fp16, two keys per dword, per quant group
+    // P * scale_v * 2^kv in fp16, two keys per dword, per quant group
     const uint32_t w00 = pack_h2(p[0] * vs0v[0], p[1] * vs0v[1]);
     const uint32_t w01 = pack_h2(p[2] * vs0v[2], p[3] * vs0v[3]);
     const uint32_t w10 = pack_h2(p[0] * vs1v[0], p[1] * vs1v[1]);
@@ -341,8 +363,14 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   // Waits for super-tile k (the copies issued before the last grab) and that grab; returns the
   // index of the wave's super-tile number k + 2: static below NS, else the grabbed value past the
   // static ones, clamped to (nxt, T] so that the loop always advances and every copy address
-  // stays inside the sequence.
+  // stays inside the sequence. No copies are issued for super-tiles past the end (T): when the
+  // next super-tile is one, the wait is for everything outstanding and k + 2 is past the end too
+  // (g is not read on that path: the grab of k + 2 was issued with no active lane).
   auto landed = [&](uint32_t& g, int k2, int nxt_tile) {
+    if (nxt_tile >= T) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      return T;
+    }
     int v;
     asm volatile("s_waitcnt vmcnt(20)\n\tv_readfirstlane_b32 %0, %1" : "=s"(v), "+v"(g) :: "memory");
     const int t = k2 < NS ? gw + k2 * NWS : NS * NWS + v;
@@ -373,10 +401,19 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
                  4u * (uint32_t)min(lane, max(nf, 1) - 1), lds_addr(&nsm.inv_freq[wv][0]));
     }
   }
-  issue(cur, B0);
-  grab(g, 2 >= NS);  // super-tile number 2: dynamic when NS == 2
-  issue(nxt, B1);
-  asm volatile("s_waitcnt vmcnt(41)" ::: "memory");  // the q and new rows have landed
+  // The grabs are issued on every path (with no active lane when static or past the end), so
+  // that the asm statement that defines g is the same on every path: its result lands in that
+  // register after the statement, and a copy the compiler might insert would read it too early.
+  if (cur < T) issue(cur, B0);
+  grab(g, 2 >= NS && nxt < T);  // super-tile number 2: dynamic when NS == 2
+  if (nxt < T) issue(nxt, B1);
+  // the q and new rows have landed (the copies and the grab issued after them may be in flight)
+  if (nxt < T)
+    asm volatile("s_waitcnt vmcnt(41)" ::: "memory");
+  else if (cur < T)
+    asm volatile("s_waitcnt vmcnt(21)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
   if constexpr (NORM) {
     // Raw q rows and new K row -> RMSNorm + RoPE at position n - 1. Row j (q rows 0 .. R - 1, the
     // K row as j = R) is done by wave j % NWAVE from its own staged copy and written into every
@@ -397,23 +434,33 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     __syncthreads();
   }
 
-  // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt
+  // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt, times
+  // the wave's power-of-two q factor (every lane reads a whole row; lanes 4 apart hold all rows)
   {
     const bool on = qvalid && mt == lq4;
     const uint8_t* qr = reinterpret_cast<const uint8_t*>(&tm) + (gh * L + qi) * 2 * D;
-    float sg[2] = {0.f, 0.f};
+    uint32_t w[64];
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
       const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * st);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      w[4 * st] = u.x;
+      w[4 * st + 1] = u.y;
+      w[4 * st + 2] = u.z;
+      w[4 * st + 3] = u.w;
+    }
+    uint32_t mbits = 0u;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const _Float16 lo = (_Float16)bf16_to_f32((uint16_t)(w[j] & 0xffffu));
-        const _Float16 hi = (_Float16)bf16_to_f32((uint16_t)(w[j] >> 16));
-        qb[st][2 * j] = on ? lo : (_Float16)0.0f;
-        qb[st][2 * j + 1] = on ? hi : (_Float16)0.0f;
-        sg[st >> 3] += (float)lo + (float)hi;
-      }
+    for (int i = 0; i < 64; ++i) mbits = bf16x2_absmax_bits(mbits, w[i]);
+    const int kq = q_pow2_exp(qvalid ? bf16x2_max_value(mbits) : 0.0f);
+    const float qf = pow2f(kq);
+    kscale = qk_scale_log2 * pow2f(24 - kq);
+    float sg[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const float lo = bf16_lo(w[i]), hi = bf16_hi(w[i]);
+      sg[i >> 5] += lo + hi;
+      qb[i >> 2][2 * (i & 3)] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
+      qb[i >> 2][2 * (i & 3) + 1] = on ? (_Float16)(hi * qf) : (_Float16)0.0f;
     }
     qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
     qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
@@ -448,8 +495,10 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   };
 
   // Unrolled by two so that each buffer's LDS offsets are constants. Step k waits for super-tile
-  // k, processes it, then refills its buffer with super-tile k + 2 (past the end the copies clamp
-  // to the last row and are never read) after the grab of super-tile k + 3.
+  // k, processes it, then refills its buffer with super-tile k + 2 after the grab of super-tile
+  // k + 3; once k + 2 is past the end (the tile counter ran out, so k + 3 would be too) no copies
+  // are issued and the grab has no active lane, so the wave's last wait finds nothing else in
+  // flight.
   for (;;) {
     if (cur >= T) break;
     int after = landed(g, k + 2, nxt);
@@ -459,8 +508,8 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     }
     process(cur, B0);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of the buffer refilled next are done
-    grab(g, k + 3 >= NS);
-    issue(after, B0);
+    grab(g, k + 3 >= NS && after < T);
+    if (after < T) issue(after, B0);
     cur = nxt;
     nxt = after;
     ++k;
@@ -472,8 +521,8 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     }
     process(cur, B1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    grab(g, k + 3 >= NS);
-    issue(after, B1);
+    grab(g, k + 3 >= NS && after < T);
+    if (after < T) issue(after, B1);
     cur = nxt;
     nxt = after;
     ++k;
@@ -492,6 +541,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     }
   }
 
+  vscale_remove(vsc, oacc);
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below
   packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.acc[0][0][0],
                        &sm.st[0][0][0], &sh_last, args, plan, x, b, hk, R);

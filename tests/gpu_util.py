@@ -34,12 +34,12 @@ def special_rows(D=128):
     return Q.round_bf16(np.stack(rows).astype(np.float32))
 
 
-def make_cache(rng, B, Hkv, n, cap, dev, bits=8, D=128):
+def make_cache(rng, B, Hkv, n, cap, dev, bits=8, D=128, kstd=1.0, vstd=1.0):
     """Random N(0,1) bf16 K/V quantized on the GPU into full-capacity buffers (rows >= n hold
     garbage codes so a kernel that reads past n is caught)."""
     out = []
-    for _ in range(2):
-        x = Q.randn_bf16(rng, (B, Hkv, n, D))
+    for std in (kstd, vstd):
+        x = Q.round_bf16(Q.randn_bf16(rng, (B, Hkv, n, D)) * np.float32(std))
         codes = torch.randint(0, 256, (B, Hkv, cap, D * bits // 8), dtype=torch.uint8, device=dev)
         sc = to_dev_bf16(rng.standard_normal((B, Hkv, cap, D // 64)) * 100, dev)
         bi = to_dev_bf16(rng.standard_normal((B, Hkv, cap, D // 64)) * 100, dev)
