@@ -302,6 +302,23 @@ int lq_gemv_norm_rope(const uint16_t* W, const uint16_t* x, const uint16_t* norm
                       const float* inv_freq, int64_t rot_dims, float mscale, int64_t offset,
                       const int32_t* offsets, uint32_t* counters, void* stream);
 
+/*
+ * No counterpart in the reference: lq_q8_decode_append_attn without a caller workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation). Same arguments, results and errors otherwise. The workspace is a static
+ * 4 MiB device array, one per GPU the library runs on, held until the process ends; a call that
+ * would need more (lq_decode_workspace_bytes of its shape) returns LQ_EWORKSPACE before any launch
+ * (32q/8kv at any length needs about 0.66 MiB). The first call on a device queues a clear of the
+ * array's counters on its stream; every call leaves them clear. All calls on one GPU share the
+ * array: calls that overlap on one GPU (concurrent streams) race.
+ */
+int lq_q8_decode_append_attn_noalloc(const uint16_t* q, const uint16_t* k_new,
+                                     const uint16_t* v_new, uint8_t* kc, uint16_t* ks,
+                                     uint16_t* kb, uint8_t* vc, uint16_t* vs, uint16_t* vb,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap,
+                                     int64_t n, const int32_t* lens_host, float scale,
+                                     uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

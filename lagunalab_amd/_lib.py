@@ -58,6 +58,8 @@ SIGNATURES = {
                                 i64, vp, vp, vp]),
     "lq_q8_decode_append_attn_pos": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
                                            i64, i64, vp, f32, vp, vp, i64, vp]),
+    "lq_q8_decode_append_attn_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64,
+                                               i64, i64, i64, vp, f32, vp, vp]),
 }
 
 _lib = None

@@ -10,6 +10,8 @@
 //    query heads of that KV head, so every K/V byte is read from HBM exactly once; the grid is
 //    one wave of resident workgroups over all CUs, for uniform and ragged batches alike (make_plan);
 //  * the merge: partials (m, l, acc[128]) per (split, query row) are combined per sequence.
+#include <mutex>
+
 #include "common.h"
 #include "qattn.h"
 
@@ -396,4 +398,98 @@ extern "C" int lq_q8_decode_append_attn_pos(const uint16_t* q, const uint16_t* k
   return decode_attn(LQ_KV_Q8, q, kc, ks, kb, vc, vs, vb, k_new, v_new, B, Hq, Hkv, D, cap,
                      n_plan + 1, nullptr, scale, out, workspace, workspace_bytes,
                      (hipStream_t)stream, pos);
+}
+
+// ----------------------------------------------------------------------------------------------
+// The fused decode step without a caller workspace, for callers that cannot allocate (code under
+// HIP graph capture, serving loops that forbid allocation). Its workspace -- the arrival and tile
+// counters, then the split partials -- is a static device array, one per GPU the library runs on,
+// held until the process ends.
+// ----------------------------------------------------------------------------------------------
+
+namespace lq {
+namespace {
+
+constexpr int64_t SCRATCH_BYTES = 4 << 20;  // 4 MiB: ~7,800 partial rows after the counters
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES];  // this device's copy of `scratch`, from hipGetSymbolAddress
+bool scratch_cleared[MAX_DEVICES];
+
+__global__ void clear_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Zeroes the counter area of the scratch on `st` (a fill kernel, so that a caller's graph capture
+// records no memset node).
+int clear_scratch_counters(void* p, hipStream_t st) {
+  hipLaunchKernelGGL(clear_words_kernel, dim3(32), dim3(256), 0, st, static_cast<uint32_t*>(p),
+                     (int)(WS_COUNTER_BYTES / 4));
+  LQ_CHECK_LAUNCH("clear_words_kernel");
+  return LQ_OK;
+}
+
+// The current device's scratch address (looked up once per device with that device current,
+// kept for later calls); on its first use the counter area is cleared on `st`.
+int current_scratch(hipStream_t st, void** out) {
+  int dev = 0;
+  LQ_CHECK_HIP(hipGetDevice(&dev));
+  LQ_CHECK_ARG(dev >= 0 && dev < MAX_DEVICES, "device %d outside [0, %d)", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    LQ_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    LQ_CHECK_ARG(p != nullptr, "no device address for the static scratch");
+    scratch_ptr[dev] = p;
+  }
+  if (!scratch_cleared[dev]) {
+    const int st_clear = clear_scratch_counters(scratch_ptr[dev], st);
+    if (st_clear != LQ_OK) return st_clear;
+    scratch_cleared[dev] = true;
+  }
+  *out = scratch_ptr[dev];
+  return LQ_OK;
+}
+
+}  // namespace
+}  // namespace lq
+
+extern "C" int lq_q8_decode_append_attn_noalloc(const uint16_t* q, const uint16_t* k_new,
+                                                const uint16_t* v_new, uint8_t* kc, uint16_t* ks,
+                                                uint16_t* kb, uint8_t* vc, uint16_t* vs,
+                                                uint16_t* vb, int64_t B, int64_t Hq, int64_t Hkv,
+                                                int64_t D, int64_t cap, int64_t n,
+                                                const int32_t* lens_host, float scale,
+                                                uint16_t* out, void* stream) {
+  using namespace lq;
+  clear_error();
+  LQ_CHECK_ARG(B >= 1 && B <= LQ_MAX_SEQS, "batch %lld outside [1, %d]", (long long)B, LQ_MAX_SEQS);
+  // the workspace this call needs (lengths after the append), against the scratch's size
+  int32_t after[LQ_MAX_SEQS];
+  if (lens_host)
+    for (int64_t b = 0; b < B; ++b) after[b] = lens_host[b] + 1;
+  const int64_t need = lq_decode_workspace_bytes(LQ_KV_Q8, B, Hq, Hkv, D, n + 1,
+                                                 lens_host ? after : nullptr);
+  if (need < 0) return LQ_EINVAL;  // error set
+  if (need > SCRATCH_BYTES) {
+    set_error("this call needs a %lld-byte workspace; the static scratch of "
+              "lq_q8_decode_append_attn_noalloc holds %lld bytes (call lq_q8_decode_append_attn "
+              "with a workspace instead)",
+              (long long)need, (long long)SCRATCH_BYTES);
+    return LQ_EWORKSPACE;
+  }
+  void* ws = nullptr;
+  const hipStream_t st = (hipStream_t)stream;
+  int rc = current_scratch(st, &ws);
+  if (rc != LQ_OK) return rc;
+  rc = lq_q8_decode_append_attn(q, k_new, v_new, kc, ks, kb, vc, vs, vb, B, Hq, Hkv, D, cap, n,
+                                lens_host, scale, out, ws, SCRATCH_BYTES, stream);
+  if (rc == LQ_EHIP) {  // a launch may have left counters set: clear them for the next call
+    std::string msg = lq_last_error();
+    clear_scratch_counters(ws, st);
+    set_error("%s", msg.c_str());
+  }
+  return rc;
 }
