@@ -42,10 +42,9 @@ namespace {
 
 using namespace attn;
 
-constexpr int DW = 4;  // waves per workgroup
-
-// ST keys per super-tile: 64 (one workgroup per CU) or 32 (about 80 KB of LDS per workgroup, two
-// workgroups per CU: two waves per SIMD hide each other's MFMA, LDS and exp latency).
+// ST keys per super-tile: 64 with DW = 4 waves per workgroup, or 32 with DW = 8 (two waves per
+// SIMD hide each other's MFMA, LDS and exp latency). Either way one workgroup per CU (about 150 KB
+// of LDS: two tile buffers per wave).
 template <int ST>
 struct DenseBuf {
   uint8_t k[ST * D];
@@ -64,14 +63,14 @@ struct DenseTerms {  // per key of the current super-tile
 
 constexpr int MAX_NEW = 16;  // rows of a fused append (verify L <= 16)
 
-template <int NT, int ST>
+template <int NT, int ST, int DW>
 struct DenseSmem {
   union {
     struct {
       DenseBuf<ST> buf[DW][2];
       DenseTerms<ST> terms[DW];
     } loop;
-    alignas(16) float acc[DW][16 * NT][D];  // wave partials (epilogue)
+    f4_t acc[DW][NT * 8][64];  // wave partials in register layout (epilogue)
   };
   alignas(16) float st[DW][16 * NT][4];  // m, l, bias sum 0, bias sum 1
   struct {                             // fused append: new row n - L + j, quantized
@@ -89,9 +88,8 @@ __device__ __forceinline__ void dma_b32_v(const void* g, uint32_t lds) {
                :: "v"(g), "s"(lds) : "memory");
 }
 
-template <int NT, bool CAUSAL, int ST>
-__global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kernel(AttnArgs args,
-                                                                                 DecodePlan plan) {
+template <int NT, bool CAUSAL, int ST, int DW>
+__global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args, DecodePlan plan) {
   static_assert(ST == 32 || ST == 64, "super-tiles of 32 or 64 keys");
   constexpr int MT = ST / 16;  // M tiles (16 keys) per super-tile
   constexpr int EK = ST / 32;  // P.V k-steps (32 keys) per super-tile
@@ -101,7 +99,7 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
   using DenseBuf = lq::DenseBuf<ST>;
   using DenseTerms = lq::DenseTerms<ST>;
   constexpr int DST = ST;
-  __shared__ DenseSmem<NT, ST> sm;
+  __shared__ DenseSmem<NT, ST, DW> sm;
   const uint16_t* __restrict__ q = args.q;
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
@@ -337,18 +335,21 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v = fmaf(s0v[r], c[mt][nt][0][r],
-                         fmaf(s1v[r], c[mt][nt][1][r],
-                              fmaf(u1v[r], qsum[nt][1], u0v[r] * qsum[nt][0])));
-          if (!full) {
-            const int t = t0 + k0 + r;
-            bool ok = t < n;
-            if (CAUSAL) ok = ok && t <= causal_base + qpos[nt];
-            v = ok ? v : -INFINITY;
-          }
-          sc[nt][mt][r] = v;
-        }
+        for (int r = 0; r < 4; ++r)
+          sc[nt][mt][r] = fmaf(s0v[r], c[mt][nt][0][r],
+                               fmaf(s1v[r], c[mt][nt][1][r],
+                                    fmaf(u1v[r], qsum[nt][1], u0v[r] * qsum[nt][0])));
+    }
+    if (!full) {  // keys past the sequence or the row's causal bound (the last super-tiles only)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int lim = CAUSAL ? causal_base + qpos[nt] : n - 1;  // <= n - 1
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sc[nt][mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim ? sc[nt][mt][r] : -INFINITY;
+      }
     }
     uint32_t pw[NT][EK][2][4];  // P.V B operands: [nt][k-step e][group][dword]
 #pragma unroll
@@ -620,39 +621,42 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
     bsum[nt][1] = sum_xor32(sum_xor16(bsum[nt][1]));
   }
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below
+  // Wave partials go to LDS as the registers hold them (lane-contiguous 16-byte writes, no bank
+  // conflicts): acc[w][8 nt + dt][lane] = oacc[nt][dt] of wave w.
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int col = nt * 16 + lc;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sm.acc[wv][col][16 * dt + 4 * lq4 + r] = oacc[nt][dt][r];
-    if (lq4 == 0) {
-      float* st = sm.st[wv][col];
-      st[0] = m_run[nt];
-      st[1] = lsum[nt];
-      st[2] = bsum[nt][0];
-      st[3] = bsum[nt][1];
-    }
+    for (int dt = 0; dt < 8; ++dt) sm.acc[wv][8 * nt + dt][lane] = oacc[nt][dt];
+    if (lq4 == 0)
+      *reinterpret_cast<float4*>(sm.st[wv][nt * 16 + lc]) =
+          make_float4(m_run[nt], lsum[nt], bsum[nt][0], bsum[nt][1]);
   }
   __syncthreads();
 
-  // ---- merge the waves (log-sum-exp) into the workgroup's partial
-  for (int o = tid; o < R * D; o += 64 * DW) {
-    const int col = o / D;
-    const int d = o - col * D;
-    const int g = d >> 6;
+  // ---- merge the waves (log-sum-exp) into the workgroup's partial, in the same layout: item
+  // (8 nt + dt, lane) holds dims 16 dt + 4 (lane / 16) + (0..3) of query row 16 nt + lane % 16
+  for (int it = tid; it < NT * 8 * 64; it += 64 * DW) {
+    const int reg = it >> 6, ln = it & 63;
+    const int col = 16 * (reg >> 3) + (ln & 15);
+    if (col >= R) continue;
+    const int dt = reg & 7;
+    const int g = dt >> 2;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    float a = 0.0f;
+    f4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < DW; ++w) {
       const float* st = sm.st[w][col];
       const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
-      a += e * fmaf(sm.acc[w][col][d], 16777216.0f, st[2 + g]);
+      const f4_t v = sm.acc[w][reg][ln];
+      const float bias = st[2 + g];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a[r] += e * fmaf(v[r], 16777216.0f, bias);
     }
-    args.part_acc[((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d] = a;
+    const int d0 = 16 * dt + 4 * (ln >> 4);
+    *reinterpret_cast<f4_t*>(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D +
+                             d0) = a;
   }
   if (tid < R) {
     const int col = tid;
@@ -671,25 +675,27 @@ __global__ __launch_bounds__(64 * DW, ST == 32 ? 2 : 1) void q8_attn_dense_kerne
 
 }  // namespace
 
-// Up to 32 query rows per KV head: 32-key super-tiles, two workgroups per CU. More rows: 64-key
-// super-tiles (their wave partials need the LDS of a whole CU).
+// Up to 32 query rows per KV head: 32-key super-tiles on 8 waves. More rows: 64-key super-tiles
+// on 4 waves (their accumulators leave no registers for a second wave per SIMD).
 QAttnFn q8_dense_attn_fn(int nt, bool causal) {
   if (causal) {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, true, 32>;
-      case 2: return q8_attn_dense_kernel<2, true, 32>;
-      case 3: return q8_attn_dense_kernel<3, true, 64>;
-      case 4: return q8_attn_dense_kernel<4, true, 64>;
+      case 1: return q8_attn_dense_kernel<1, true, 32, 8>;
+      case 2: return q8_attn_dense_kernel<2, true, 32, 8>;
+      case 3: return q8_attn_dense_kernel<3, true, 64, 4>;
+      case 4: return q8_attn_dense_kernel<4, true, 64, 4>;
     }
   } else {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, false, 32>;
-      case 2: return q8_attn_dense_kernel<2, false, 32>;
-      case 3: return q8_attn_dense_kernel<3, false, 64>;
-      case 4: return q8_attn_dense_kernel<4, false, 64>;
+      case 1: return q8_attn_dense_kernel<1, false, 32, 8>;
+      case 2: return q8_attn_dense_kernel<2, false, 32, 8>;
+      case 3: return q8_attn_dense_kernel<3, false, 64, 4>;
+      case 4: return q8_attn_dense_kernel<4, false, 64, 4>;
     }
   }
   return nullptr;
 }
+
+int q8_dense_threads(int nt) { return nt <= 2 ? 512 : 256; }
 
 }  // namespace lq

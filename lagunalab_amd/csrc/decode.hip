@@ -188,7 +188,10 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   const int64_t R = (Hq / Hkv) * L;
   if (kind == LQ_KV_Q8) {
     const int nt = (int)((R + 15) / 16);
-    k = {attn_merges_itself(R) ? q8_attn_fn(L > 1) : q8_dense_attn_fn(nt, L > 1), 256};
+    if (attn_merges_itself(R))
+      k = {q8_attn_fn(L > 1), 256};
+    else
+      k = {q8_dense_attn_fn(nt, L > 1), q8_dense_threads(nt)};
   } else if (kind == LQ_KV_BF16 && R <= 4) {
     k = {bf16_attn_fn(L > 1), 128};
   } else if (kind == LQ_KV_Q4 && R <= 4) {
@@ -198,8 +201,7 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   }
   if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
-  // One workgroup per CU for the dense kernel too: with 32-key super-tiles two would fit, but
-  // measured at 65,541 keys and 20 rows per KV head, 32 splits per head (36.4 us) beat 64 (37.8).
+  // One workgroup per CU for the dense kernel too (its 8 or 4 waves hold about 150 KB of LDS).
   const int per_cu = attn_merges_itself(R) || kind != LQ_KV_Q8 ? attn_occupancy(k.fn, k.threads) : 1;
   const int64_t S = make_plan(B, Hkv, n, lens, cap, per_cu * device_cu_count(),
                               kind == LQ_KV_Q8, attn_merges_itself(R) ? MAX_SPLITS : MERGE_SPLITS,

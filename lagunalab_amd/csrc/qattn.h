@@ -87,6 +87,8 @@ void launch_q8_attn_norm(unsigned S, unsigned Hkv, hipStream_t st, const AttnArg
 // Dense-layout kernel (attn_dense.hip) for 4 < G * L <= 16 nt rows per KV head; partials merged
 // by decode_merge_kernel.
 QAttnFn q8_dense_attn_fn(int nt, bool causal);
+// Its workgroup size for nt column tiles.
+int q8_dense_threads(int nt);
 
 // The attention kernel for one call: its function and workgroup size.
 struct AttnKernel {
