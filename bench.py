@@ -56,14 +56,15 @@ def parse():
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "q4", "bf16", "ragged", "verify", "lookup", "layers",
-                            "prefill"],
+                            "prefill", "quantize"],
                    help="decode: the 8-bit decode step (default). q4 / bf16: decode attention over "
                         "a 4-bit / plain bf16 cache at the same context. ragged: 8 sequences of "
                         "default_rng(1) lengths in [42771, 82671]. verify: a 5-row causal verify "
                         "block over 65,536 cached rows plus its append. lookup: n-gram draft search "
                         "over 82,671 ids and greedy accept of 5 x 131,072 logits. layers: one decoded "
                         "token through the attention blocks of --layers full-attention layers. "
-                        "prefill: a 2,048-row chunk appended and attended at --ctx rows")
+                        "prefill: a 2,048-row chunk appended and attended at --ctx rows. "
+                        "quantize: bulk quantize-append of --ctx K and V rows (8 heads, one launch)")
     return p.parse_args()
 
 
@@ -606,6 +607,56 @@ def run_workload(args):
                              f"{HQ}q/{HKV}kv heads, head_dim {D}, YaRN RoPE 0.5, per-head gate, "
                              f"8-bit cache of {n0} rows each), one HIP graph per token",
                  "ctx": n0, "layers": nl, "hidden": C}, extra)
+        return
+
+    if args.workload == "quantize":
+        # the prefill / growth path: K and V rows of all 8 heads quantized into the cache at once
+        rows = args.ctx
+        cap = (rows + 255) // 256 * 256
+        k = torch.randn((1, HKV, rows, D), device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn((1, HKV, rows, D), device=dev, generator=g).to(torch.bfloat16)
+
+        def bufs():
+            return (torch.zeros((1, HKV, cap, D), dtype=torch.uint8, device=dev),
+                    torch.zeros((1, HKV, cap, D // GS), dtype=torch.bfloat16, device=dev),
+                    torch.zeros((1, HKV, cap, D // GS), dtype=torch.bfloat16, device=dev))
+        kq, vq = bufs(), bufs()
+
+        def call(j):
+            st = lib.lq_quantize_append_kv(k.data_ptr(), v.data_ptr(), 1, HKV, rows, D,
+                                           kq[0].data_ptr(), kq[1].data_ptr(), kq[2].data_ptr(),
+                                           vq[0].data_ptr(), vq[1].data_ptr(), vq[2].data_ptr(),
+                                           cap, 0, 8, GS, sp)
+            if st:
+                _lib.check(st, "lq_quantize_append_kv")
+        for j in range(args.warmup):
+            call(j)
+        torch.cuda.synchronize()
+        per = _gpu_groups(stream, args.steps, 4, call)
+        ms = sum(per) / len(per)
+        vals = 2 * HKV * rows * D
+        nbytes = vals * 3 + 2 * HKV * rows * (D // GS) * 4  # bf16 in, codes out, bf16 scale + bias
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        extra = {"us_per_call": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                              "kernel": "lq_quantize_append_kv (8-bit, group 64)",
+                              "bytes_per_call": nbytes}}
+        if do_cpu:
+            from oracle import quantize as OQ
+            sample = 4096  # rows per head of K
+            xs = k[0, :, :sample].float().cpu().numpy()
+            t, calls = _time_cpu(lambda: OQ.quantize_packed(xs, GS, 8), min(20.0, args.cpu_seconds))
+            sbytes = HKV * sample * D * 3 + HKV * sample * (D // GS) * 4
+            extra["cpu_baseline"] = {
+                "value": round(sbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "us_per_call": round(t * 1e6, 1),
+                "sample": f"median of {calls} calls of the NumPy quantizer on 8 heads x {sample} rows "
+                          f"of K (one thread); CPU: {_cpu_model()}"}
+        _result(f"bulk 8-bit quantize-append GB/s ({rows:,} K and V rows x 8 heads)", round(gbs, 2),
+                "GB/s", True, ms, args, "u8",
+                {"workload": f"quantize-append of {rows} K and V rows, {HKV} heads, head_dim {D}, "
+                             f"group {GS}, one launch", "rows": rows}, extra)
         return
 
     if args.workload == "lookup":

@@ -124,6 +124,8 @@ constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
 constexpr int DPP_ROW_ROR4 = 0x124;   // row_ror:4
 constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i of a row <- lane 15 - i
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i of a half row <- lane 7 - i
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

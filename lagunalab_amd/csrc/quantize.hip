@@ -1,11 +1,12 @@
 // Quantize-on-append and dequantize for the affine group-quantized KV cache.
 //
 // lq_quantize_append replaces mx.quantize as called by mlx-lm QuantizedKVCache.update_and_fetch
-// from DequantKVCache.update_and_fetch (laguna_mlx/cache.py:89-90). One wave64 owns one group
-// (32, 64 or 128 values): the group min/max are wave reductions, then every lane derives the same
-// scale/bias with IEEE fp32 arithmetic (correctly rounded division, round-half-away), writes its
-// codes, and lane 0 writes the bf16 scale and bias. The arithmetic is bit-for-bit the MLX affine
-// quantizer restated in oracle/quantize.py.
+// from DequantKVCache.update_and_fetch (laguna_mlx/cache.py:89-90). A lane takes 8 consecutive
+// values of a row (one 16-byte load) and the gs / 8 lanes of a group (32, 64 or 128 values, side
+// by side in one wave) reduce its min and max with DPP; every lane then derives the group's
+// scale/bias with IEEE fp32 arithmetic (correctly rounded division, round-half-away) and writes
+// its 8 codes (8 or 4 bytes), and the group's first lane writes the bf16 scale and bias. The
+// arithmetic is bit-for-bit the MLX affine quantizer restated in oracle/quantize.py.
 //
 // lq_dequantize replaces mx.dequantize on the unfused path (cache.py:99-100):
 // bf16(fp32(scale) * code + fp32(bias)) with an unfused multiply then add.
@@ -14,75 +15,129 @@
 namespace lq {
 namespace {
 
-constexpr int kWaves = 4;  // waves (groups) per 256-thread block
+// Unsigned division by a fixed divisor d >= 1 of values below 2^31: q = (mulhi(n, m) + n) >> l
+// with 2^(l-1) < d <= 2^l and m = floor(2^32 (2^l - d) / d) + 1 (Granlund and Montgomery, 1994).
+struct FastDiv {
+  uint32_t m, l;
+};
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return {(uint32_t)m, l};
+}
+__device__ __forceinline__ uint32_t fdiv_u(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.m) + n) >> f.l;
+}
 
-// EPL: elements per lane (group_size / 64, at least 1). BITS: 4 or 8.
-// Groups [0, ngroups) go to target a, groups [ngroups, 2 ngroups) to target b when `two` (K and
-// V of one update in a single launch).
-template <int EPL, int BITS>
+// Code of one value: round-half-away(fl(fl(x - bias) / scale)) clamped to 2^BITS - 1, as
+// affine_code. Fast path: u = (x - bias) * (1 / scale) + 0.5 (v_rcp_f32, 1 ulp) is within
+// 6.1e-5 of fl(fl(x - bias) / scale) + 0.5 for quotients below 512 (ours stay below 257), so
+// floor(u) is the code unless u lies within 2e-4 of an integer; those lanes (and NaN/inf) take the
+// correctly rounded division instead. Returns the code; sets `slow` for the lanes that need it.
+template <int BITS>
+__device__ __forceinline__ uint32_t fast_code(float x, const AffineParams& p, float rs, bool& slow) {
+  constexpr float n_bins = (float)((1 << BITS) - 1);
+  const float u = fmaf(x - p.bias, rs, 0.5f);
+  const float f = u - floorf(u);
+  slow = !(fabsf(f - 0.5f) < 0.4998f);
+  return (uint32_t)fminf(floorf(u), n_bins);
+}
+
+// LPG = group_size / 8 lanes per group; UN chunks of 8 values per lane per pass (loads issued
+// together). Chunks [0, chunks) go to target a, [chunks, 2 chunks) to target b when `two` (K and V
+// of one update in one launch). Chunk c of a target: row c / cpr (row = bh L + l, cache row
+// bh cap + offset + l), values 8 (c % cpr) .. + 7.
+template <int BITS, int LPG, int UN>
 __global__ __launch_bounds__(256) void quantize_append_kernel(
-    AppendTarget a, AppendTarget b, int two, int64_t ngroups, int gs, int groups_per_row,
-    int64_t L, int64_t cap, int64_t offset) {
+    AppendTarget a, AppendTarget b, int64_t chunks, int64_t total, FastDiv fd_cpr, FastDiv fd_L,
+    int cpr, int L, int64_t cap, int64_t offset) {
   const int lane = threadIdx.x & 63;
-  int64_t gi = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (gi >= (two ? 2 * ngroups : ngroups)) return;  // whole wave exits together (wave-uniform)
-  const bool second = gi >= ngroups;
-  if (second) gi -= ngroups;
-  const uint16_t* __restrict__ src = second ? b.src : a.src;
-  uint8_t* __restrict__ codes = second ? b.codes : a.codes;
-  uint16_t* __restrict__ scales = second ? b.scales : a.scales;
-  uint16_t* __restrict__ biases = second ? b.biases : a.biases;
-
-  const bool has = lane * EPL < gs;
-  float x[EPL];
-  float lo = INFINITY, hi = -INFINITY;
-  const uint16_t* g = src + gi * gs;
+  const int gpr = cpr / LPG;  // groups per row
+  const int64_t stride = (int64_t)gridDim.x * 256 * UN;
+  for (int64_t base = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 * UN; base < total;
+       base += stride) {  // wave-uniform
+    uint4 raw[UN];
+    int64_t cc[UN];
+    bool sec[UN], in[UN];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    x[e] = has ? bf16_to_f32(g[lane * EPL + e]) : 0.0f;
-    if (has) {
-      lo = fminf(lo, x[e]);
-      hi = fmaxf(hi, x[e]);
+    for (int u = 0; u < UN; ++u) {
+      const int64_t i = base + 64 * u + lane;
+      in[u] = i < total;
+      sec[u] = i >= chunks;
+      cc[u] = sec[u] ? i - chunks : i;
+      const uint16_t* src = sec[u] ? b.src : a.src;
+      raw[u] = in[u] ? *reinterpret_cast<const uint4*>(src + cc[u] * 8) : make_uint4(0u, 0u, 0u, 0u);
     }
-  }
-  const float w_min = wave_min(lo);
-  const float w_max = wave_max(hi);
-
-  const AffineParams p = affine_params<BITS>(w_min, w_max);
-  const float scale = p.scale, bias = p.bias;
-
-  uint32_t c[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) c[e] = affine_code<BITS>(x[e], p);
-
-  // destination row in the cache
-  const int64_t row = gi / groups_per_row;
-  const int gr = (int)(gi - row * groups_per_row);
-  const int64_t bh = row / L;
-  const int64_t l = row - bh * L;
-  const int64_t drow = bh * cap + offset + l;
-  const int64_t row_bytes = (int64_t)groups_per_row * gs * BITS / 8;
-  uint8_t* dst = codes + drow * row_bytes + (int64_t)gr * (gs * BITS / 8);
-
-  if (BITS == 8) {
-    if (has) {
-      if (EPL == 1) {
-        dst[lane] = (uint8_t)c[0];
-      } else {  // EPL == 2
-        *reinterpret_cast<uint16_t*>(dst + 2 * lane) = (uint16_t)(c[0] | (c[EPL - 1] << 8));
+    for (int u = 0; u < UN; ++u) {
+      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[2 * j] = bf16_lo(w[j]);
+        x[2 * j + 1] = bf16_hi(w[j]);
+      }
+      float lo = INFINITY, hi = -INFINITY;
+      if (in[u]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          lo = fminf(lo, x[j]);
+          hi = fmaxf(hi, x[j]);
+        }
+      }
+      // group min / max over its LPG lanes (quads, then half rows, then rows)
+      lo = fminf(lo, dpp<DPP_QUAD_XOR1>(lo));
+      hi = fmaxf(hi, dpp<DPP_QUAD_XOR1>(hi));
+      lo = fminf(lo, dpp<DPP_QUAD_XOR2>(lo));
+      hi = fmaxf(hi, dpp<DPP_QUAD_XOR2>(hi));
+      if (LPG >= 8) {
+        lo = fminf(lo, dpp<DPP_ROW_HALF_MIRROR>(lo));
+        hi = fmaxf(hi, dpp<DPP_ROW_HALF_MIRROR>(hi));
+      }
+      if (LPG >= 16) {
+        lo = fminf(lo, dpp<DPP_ROW_MIRROR>(lo));
+        hi = fmaxf(hi, dpp<DPP_ROW_MIRROR>(hi));
+      }
+      const AffineParams p = affine_params<BITS>(lo, hi);
+      const float rs = __builtin_amdgcn_rcpf(p.scale);
+      uint32_t c[8];
+      bool any_slow = false, slow[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        c[j] = fast_code<BITS>(x[j], p, rs, slow[j]);
+        any_slow |= slow[j];
+      }
+      if (__builtin_amdgcn_ballot_w64(any_slow && in[u])) {  // rare: a value near a rounding edge
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (slow[j]) c[j] = affine_code<BITS>(x[j], p);
+      }
+      if (in[u]) {
+        const uint32_t cu = (uint32_t)cc[u];
+        const uint32_t row = fdiv_u(cu, fd_cpr);
+        const int ch = (int)(cu - row * (uint32_t)cpr);
+        const uint32_t bh = fdiv_u(row, fd_L);
+        const int64_t drow = (int64_t)bh * cap + offset + (int64_t)(row - bh * (uint32_t)L);
+        uint8_t* codes = sec[u] ? b.codes : a.codes;
+        if (BITS == 8) {
+          const uint32_t d0 = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+          const uint32_t d1 = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+          *reinterpret_cast<uint2*>(codes + drow * (8 * cpr) + 8 * ch) = make_uint2(d0, d1);
+        } else {  // element 2j in the low nibble of byte j
+          uint32_t d0 = 0u;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) d0 |= c[j] << (4 * j);
+          *reinterpret_cast<uint32_t*>(codes + drow * (4 * cpr) + 4 * ch) = d0;
+        }
+        if (ch % LPG == 0) {
+          uint16_t* scales = sec[u] ? b.scales : a.scales;
+          uint16_t* biases = sec[u] ? b.biases : a.biases;
+          scales[drow * gpr + ch / LPG] = f32_to_bf16(p.scale);
+          biases[drow * gpr + ch / LPG] = f32_to_bf16(p.bias);
+        }
       }
     }
-  } else {  // 4-bit: element 2j in the low nibble of byte j
-    if (EPL == 2) {
-      if (has) dst[lane] = (uint8_t)(c[0] | (c[EPL - 1] << 4));
-    } else {
-      const uint32_t nb = (uint32_t)__shfl_down((int)c[0], 1, 64);
-      if (has && (lane & 1) == 0) dst[lane >> 1] = (uint8_t)(c[0] | (nb << 4));
-    }
-  }
-  if (lane == 0) {
-    scales[drow * groups_per_row + gr] = f32_to_bf16(scale);
-    biases[drow * groups_per_row + gr] = f32_to_bf16(bias);
   }
 }
 
@@ -129,12 +184,15 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
   }
 }
 
-template <int EPL, int BITS>
-void launch_quantize(AppendTarget a, AppendTarget b, int two, int64_t ngroups, int gs, int gpr,
-                     int64_t L, int64_t cap, int64_t offset, hipStream_t st) {
-  const int64_t blocks = ((two ? 2 : 1) * ngroups + kWaves - 1) / kWaves;
-  quantize_append_kernel<EPL, BITS><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-      a, b, two, ngroups, gs, gpr, L, cap, offset);
+template <int BITS, int LPG>
+void launch_quantize(AppendTarget a, AppendTarget b, int64_t chunks, int64_t total, int cpr, int L,
+                     int64_t cap, int64_t offset, hipStream_t st) {
+  constexpr int UN = 4;
+  const int64_t waves = (total + 64 * UN - 1) / (64 * UN);
+  const int64_t blocks = std::min<int64_t>((waves + 3) / 4, 8192);
+  quantize_append_kernel<BITS, LPG, UN><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+      a, b, chunks, total, make_fastdiv((uint32_t)cpr), make_fastdiv((uint32_t)L), cpr, L, cap,
+      offset);
 }
 
 }  // namespace
@@ -154,14 +212,20 @@ int quantize_append(AppendTarget a, AppendTarget b, int two, int64_t B, int64_t 
   LQ_CHECK_ARG(a.src && a.codes && a.scales && a.biases, "null pointer");
   LQ_CHECK_ARG(!two || (b.src && b.codes && b.scales && b.biases), "null pointer");
   if (L == 0) return LQ_OK;
-  const int gpr = (int)(D / group_size);
-  const int64_t ngroups = B * H * L * gpr;
-  if (group_size == 128) {
-    if (bits == 8) launch_quantize<2, 8>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
-    else launch_quantize<2, 4>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
+  const int64_t chunks = B * H * L * (D / 8);  // 8 values each
+  const int64_t total = (two ? 2 : 1) * chunks;
+  LQ_CHECK_ARG(total < (int64_t)1 << 31 && L < (int64_t)1 << 31 && D / 8 < (int64_t)1 << 31,
+               "append of %lld values is too large for one call", (long long)(total * 8));
+  const int cpr = (int)(D / 8);
+  if (group_size == 32) {
+    if (bits == 8) launch_quantize<8, 4>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 4>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+  } else if (group_size == 64) {
+    if (bits == 8) launch_quantize<8, 8>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 8>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
   } else {
-    if (bits == 8) launch_quantize<1, 8>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
-    else launch_quantize<1, 4>(a, b, two, ngroups, group_size, gpr, L, cap, offset, st);
+    if (bits == 8) launch_quantize<8, 16>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 16>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
   }
   LQ_CHECK_LAUNCH("quantize_append_kernel");
   return LQ_OK;

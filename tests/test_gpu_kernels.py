@@ -37,6 +37,69 @@ def test_quantize_bit_exact(dev, bits, gs):
     np.testing.assert_array_equal(bits16(b), wb)
 
 
+def tie_rows(D, gs, rng, rows=64):
+    """Groups whose quotients (x - bias) / scale sit exactly on, or one bf16 step beside, the
+    half-integer rounding edges: ends -128 and 127 give scale 1 and bias -128, so x = -128 + k + 0.5
+    divides to k + 0.5 exactly (round half away from zero decides the code)."""
+    out = np.empty((rows, D), np.float32)
+    for r in range(rows):
+        g = []
+        for _ in range(D // gs):
+            v = -128.0 + rng.integers(0, 255, gs).astype(np.float32) + 0.5
+            if r % 2:  # neighbours of the edges: one bf16 step up or down
+                v = Q.round_bf16(v + np.where(rng.random(gs) < 0.5, -1, 1) * np.abs(v) * 2.0 ** -8)
+            v[0], v[1] = -128.0, 127.0
+            g.append(v)
+        out[r] = np.concatenate(g)
+    return Q.round_bf16(out)
+
+
+@pytest.mark.parametrize("bits,gs,D", [(8, 64, 128), (4, 64, 128), (8, 32, 96), (4, 32, 160),
+                                       (8, 128, 256), (4, 128, 128)])
+def test_quantize_ties_and_shapes(dev, bits, gs, D):
+    """Exact rounding ties and their neighbours, head dims whose 8-value chunks per row are not a
+    power of two, and B, H, L, offset that make every index of the row and cache-row arithmetic
+    matter: codes, scales and biases bit-exact against the oracle."""
+    from lagunalab_amd.quant import quantize_into
+    rng = np.random.default_rng(40 + bits + gs + D)
+    B, H, L, cap, off = 2, 3, 37, 50, 11
+    x = np.concatenate([tie_rows(D, gs, rng, B * H * L // 2),
+                        Q.round_bf16(Q.randn_bf16(rng, (B * H * L - B * H * L // 2, D)) * 3)])
+    x = x[rng.permutation(len(x))].reshape(B, H, L, D)
+    codes = torch.full((B, H, cap, D * bits // 8), 9, dtype=torch.uint8, device=dev)
+    sc = torch.full((B, H, cap, D // gs), 1.5, dtype=torch.bfloat16, device=dev)
+    bi = torch.full((B, H, cap, D // gs), -2.0, dtype=torch.bfloat16, device=dev)
+    quantize_into(to_dev_bf16(x, dev), codes, sc, bi, off, gs, bits)
+    wc, ws, wb = Q.quantize_packed(x, gs, bits)
+    c = codes.cpu().numpy()
+    np.testing.assert_array_equal(c[:, :, off:off + L], wc)
+    np.testing.assert_array_equal(bits16(sc)[:, :, off:off + L], ws)
+    np.testing.assert_array_equal(bits16(bi)[:, :, off:off + L], wb)
+    assert (c[:, :, :off] == 9).all() and (c[:, :, off + L:] == 9).all()
+
+
+def test_quantize_prefill_size_bit_exact(dev):
+    """A prefill-sized append (8 heads x 20,000 rows x 128, K and V in one launch: several
+    grid-stride passes per wave) bit-exact against the oracle."""
+    from lagunalab_amd.quant import quantize_kv_into
+    g = torch.Generator(device=dev).manual_seed(5)
+    H, L, cap = 8, 20000, 20224
+    k = torch.randn((1, H, L, 128), device=dev, generator=g).to(torch.bfloat16)
+    v = (torch.randn((1, H, L, 128), device=dev, generator=g) * 7).to(torch.bfloat16)
+
+    def bufs():
+        return (torch.zeros((1, H, cap, 128), dtype=torch.uint8, device=dev),
+                torch.zeros((1, H, cap, 2), dtype=torch.bfloat16, device=dev),
+                torch.zeros((1, H, cap, 2), dtype=torch.bfloat16, device=dev))
+    kq, vq = bufs(), bufs()
+    quantize_kv_into(k, v, kq, vq, 0, 64, 8)
+    for src, (c, s, b) in ((k, kq), (v, vq)):
+        wc, ws, wb = Q.quantize_packed(src.float().cpu().numpy(), 64, 8)
+        np.testing.assert_array_equal(c.cpu().numpy()[:, :, :L], wc)
+        np.testing.assert_array_equal(bits16(s)[:, :, :L], ws)
+        np.testing.assert_array_equal(bits16(b)[:, :, :L], wb)
+
+
 def test_quantize_append_writes_only_its_rows(dev):
     from lagunalab_amd.quant import quantize_into
     rng = np.random.default_rng(1)
