@@ -54,6 +54,10 @@ def parse():
                         "instead of the fused step (lq_q8_decode_append_attn)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 8 times (HBM counter calibration)")
+    p.add_argument("--q-heads", type=int, default=32,
+                   help="query heads over the 8 KV heads (decode, verify, q4, bf16, ragged): 32 is the "
+                        "benchmarked 32q/8kv shape, 48 Laguna's own 48q/8kv (the dense kernel and a "
+                        "merge launch for the 8-bit cache)")
     p.add_argument("--workload", default="decode",
                    choices=["decode", "q4", "bf16", "ragged", "verify", "lookup", "layers",
                             "prefill", "quantize"],
@@ -737,6 +741,10 @@ def main():
 
     from lagunalab_amd import _lib
 
+    global HQ
+    HQ = args.q_heads
+    if HQ % HKV or not HKV <= HQ <= 16 * HKV:
+        sys.exit(f"--q-heads must be a multiple of {HKV} in [{HKV}, {16 * HKV}]")
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
@@ -868,20 +876,26 @@ def main():
         kernel = "lq_decode_attn (q8_attn_packed_kernel, split merge fused)"
         k_ms, k_bytes, k_calls = attn_avg_ms, sum(attn_bytes) / len(attn_bytes), len(attn_ms) * group
     else:
-        kernel = "lq_q8_decode_append_attn (q8_attn_packed_kernel: append + attention + split merge)"
+        if HQ // HKV <= 4:
+            kernel = ("lq_q8_decode_append_attn (q8_attn_packed_kernel: append + attention + split "
+                      "merge)")
+        else:
+            kernel = ("lq_q8_decode_append_attn (q8_attn_dense_kernel: append + attention; "
+                      "decode_merge_kernel)")
         k_ms, k_bytes, k_calls = total_ms / args.steps, sum(step_bytes) / len(step_bytes), args.steps
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
 
     traffic = None
     tf = ROOT / "profiles" / "q8_decode_traffic.json"
-    if tf.exists():
+    if tf.exists() and HQ == 32 and not args.separate_append:
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_call")
         except Exception:
             traffic = None
 
     res = {
-        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "metric": METRIC if HQ == 32 else f"{METRIC}, {HQ}q/{HKV}kv", "value": round(value, 2),
+        "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": round(value / REF_M4_GBS, 2), "dtype": "u8",

@@ -192,8 +192,9 @@ int lq_greedy_accept(const float* logits, int64_t L, int64_t V, const int32_t* d
  * row, inv_freq fp32 [rot_dims / 2], rot_dims a multiple of 4 up to 128, rotated dims scaled by
  * mscale; the same arithmetic as lq_qk_norm_rope) before the fused append and attention of
  * lq_q8_decode_append_attn. pos: as lq_q8_decode_append_attn_pos (device append rows), or null:
- * every sequence appends at row n_plan. At most 4 query heads per KV head; workspace sized for
- * n_plan + 1 rows.
+ * every sequence appends at row n_plan. Workspace sized for n_plan + 1 rows. With more than 4 query
+ * heads per KV head the norm and RoPE run as a launch of their own before the attention kernel
+ * (their output rows live in the workspace).
  */
 int lq_q8_decode_norm_append_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                                   uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc,
@@ -209,8 +210,7 @@ int lq_q8_decode_norm_append_attn(const uint16_t* q, const uint16_t* k_new, cons
  * row each sequence appends at (its rows before the append), so that one recorded launch -- a HIP
  * graph of a decode step -- serves every step; the split plan and the workspace are those of
  * n_plan rows per sequence (size the workspace with lq_decode_workspace_bytes for n_plan + 1).
- * Each sequence attends over min(pos[b] + 1, cap) rows; keep pos[b] < cap. At most 4 query heads
- * per KV head.
+ * Each sequence attends over min(pos[b] + 1, cap) rows; keep pos[b] < cap.
  */
 int lq_q8_decode_append_attn_pos(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                                  uint8_t* kc, uint16_t* ks, uint16_t* kb, uint8_t* vc,

@@ -112,7 +112,9 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   const int hk = blockIdx.y;
   int b;
   find_seq(plan, x, b);
-  const int n = plan.len[b];
+  // rows after the append: the host's length, or (decode from device positions) pos[b] + 1
+  const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap)
+                         : plan.len[b];
   const int T = (n + DST - 1) / DST;
   const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * DW;
   const int gw = (x - plan.split_begin[b]) * DW + wv;

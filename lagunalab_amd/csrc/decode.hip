@@ -181,6 +181,10 @@ void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq
 
 bool attn_merges_itself(int64_t rows_per_kv_head) { return rows_per_kv_head <= 4; }
 
+// Decode with the dense kernel: where the q and new K rows after q/k norm + RoPE go in the
+// workspace (behind the partials, 256-byte aligned).
+int64_t norm_rows_offset(int64_t partials_end) { return (partials_end + 255) / 256 * 256; }
+
 // Shared by decode (L = 1) and verify (L <= 16): kernel choice, plan and workspace size.
 int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n,
                   const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
@@ -208,6 +212,8 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
                               plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
+  if (kind == LQ_KV_Q8 && L == 1 && !attn_merges_itself(R))  // normalized q / k rows (norm entry)
+    ws_bytes = norm_rows_offset(ws_bytes) + B * (Hq + Hkv) * D * (int64_t)sizeof(uint16_t);
   return S;
 }
 
@@ -271,12 +277,26 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
     return LQ_EWORKSPACE;
   }
   const bool fused_merge = kind != LQ_KV_Q8 || attn_merges_itself(Hq / Hkv);
-  LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new && attn_merges_itself(Hq / Hkv)),
-               "device positions need the fused 8-bit append with at most 4 query heads per KV head");
+  LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new),
+               "device positions need the fused 8-bit append");
+  LQ_CHECK_ARG(!norm || (kind == LQ_KV_Q8 && k_new), "the q/k norm needs the fused 8-bit append");
+  if (norm && !fused_merge) {
+    // Dense kernel (more than 4 query heads per KV head): q/k RMSNorm + RoPE as a launch of its
+    // own (the same arithmetic as the packed kernel's prologue) into the workspace, at the append
+    // row (device positions, or n - 1), then the fused step from those rows.
+    const int64_t parts = WS_COUNTER_BYTES + S * Hq * (int64_t)(D * sizeof(float) + sizeof(float2));
+    uint16_t* qn = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) +
+                                               norm_rows_offset(parts));
+    uint16_t* kn = qn + B * Hq * D;
+    const int rs = lq_qk_norm_rope(q, k_new, qn, kn, norm->qn_w, norm->kn_w, B, Hq, Hkv, 1, D,
+                                   norm->norm_eps, norm->inv_freq, norm->rot_dims, norm->mscale,
+                                   n - 1, pos_dev, st);
+    if (rs != LQ_OK) return rs;
+    q = qn;
+    k_new = kn;
+    norm = nullptr;
+  }
   AttnArgs a{};
-  LQ_CHECK_ARG(!norm || (kind == LQ_KV_Q8 && k_new && attn_merges_itself(Hq / Hkv)),
-               "the in-kernel q/k norm needs the fused 8-bit append with at most 4 query heads "
-               "per KV head");
   a.pos = pos_dev;
   a.q = q;
   a.kc = static_cast<uint8_t*>(kc);

@@ -193,13 +193,13 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restri
 //    [H]) or of k itself (IN 3: aux [K]), the gate softplus(logit) rounded to bf16, the product
 //    rounded to bf16 -- the gated attention output;
 //  * with `res`: y[n] = bf16(res[n] + bf16(W[n] . x)), the residual add (y may alias res).
-// Each thread first loads its two input chunks (thread t: chunks t and t + 256) and their aux
-// values, then every wave issues all its weight loads (RPW rows; lane l owns chunks l + 64 i,
-// i < NC), and while those are in flight the workgroup builds the input vector once into LDS
+// Each thread first loads its input chunks (thread t: chunks t + 256 i) and their aux values,
+// then every wave issues all its weight loads (RPW rows; lane l owns chunks l + 64 i, i < NL),
+// and while those are in flight the workgroup builds the input vector once into LDS
 // (the norm's sum of squares reduced over the workgroup); each wave then takes it from there.
 // No load sits under a branch: an index past the end is clamped to a valid address and its value
 // left unused (a branch around a load makes the compiler wait for every load in flight at the
-// join). NC > 0: K == 512 NC exactly; NC == 0: any K up to 512 MAXC, with run-time bounds.
+// join). NC > 0: K == 512 NC exactly; NC == 0: any K up to 512 NLM, with run-time bounds.
 //
 // With EPI (input projection only, two rows per wave): the first `heads` x 128 outputs are the q
 // and k heads, and each head is normalized and rotated in place (norm_rope_lane) by the last of
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restri
 // (written through to the device-coherent level), wait for them, then count their arrival on the
 // head's counter; the last arrival resets the counter to zero, and after an acquire fence its
 // first wave reads the head back and rewrites it.
-constexpr int MAXC = 8;
+constexpr int MAXC = 16;  // K <= 512 MAXC = 8192 (Laguna's 48-head o_proj: 6144)
 struct HeadEpilogue {
   const uint16_t* q_w;      // q_norm weights [128]
   const uint16_t* k_w;      // k_norm weights [128]
@@ -236,14 +236,16 @@ __device__ __forceinline__ float dot8(const uint4 w, const uint4 x, float a) {
   return a;
 }
 
-template <int RPW, int IN, bool EPI, int NC>
+template <int RPW, int IN, bool EPI, int NC, int NLM>
 __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, const uint16_t* x,
                                                          const uint16_t* aux,
                                                          const uint16_t* res, uint16_t* y, int N,
                                                          int K, float eps, HeadEpilogue epi) {
   static_assert(!EPI || (RPW == 2 && IN == 1), "the head epilogue runs on the input projection");
-  constexpr int NL = NC ? NC : MAXC;  // weight chunks per lane per row
-  __shared__ uint4 xs[64 * MAXC];
+  constexpr int NL = NC ? NC : NLM;  // weight chunks per lane per row
+  constexpr int XIN = (64 * NL + 255) / 256;  // input chunks per thread
+  static_assert(NL <= MAXC, "input wider than the staging buffer");
+  __shared__ uint4 xs[64 * NL];
   __shared__ float red[4];
   __shared__ int sh_last;
   const int tid = threadIdx.x;
@@ -254,10 +256,10 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
   const uint4* x4 = reinterpret_cast<const uint4*>(x);
   const uint4* a4 = reinterpret_cast<const uint4*>(aux);
 
-  uint4 xin[2], ain[2];
-  uint16_t gin[2];
+  uint4 xin[XIN], ain[XIN];
+  uint16_t gin[XIN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < XIN; ++i) {
     const int cc = min(tid + 256 * i, chunks - 1);
     xin[i] = x4[cc];
     if (IN == 1 || IN == 3) ain[i] = a4[cc];
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
   if (IN == 1) {
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < XIN; ++i) {
       const uint32_t xw[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
       float s = 0.0f;
 #pragma unroll
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
     inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < XIN; ++i) {
     const uint32_t xw[4] = {xin[i].x, xin[i].y, xin[i].z, xin[i].w};
     const uint32_t aw[4] = {ain[i].x, ain[i].y, ain[i].z, ain[i].w};
     uint32_t ow[4];
@@ -391,21 +393,32 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
 }
 
 // Launches gemv_fused_kernel for (N, K): two rows per wave once there are enough rows to fill the
-// chip with them (always with the head epilogue), exact-width variants for K = 2048 and 4096.
+// chip with them (always with the head epilogue), exact-width variants for K = 2048, 4096 and
+// 6144, else the narrowest run-time-bounded one (up to 2048, 4096 or 8192).
 template <int IN, bool EPI>
 void launch_gemv(const uint16_t* W, const uint16_t* x, const uint16_t* aux, const uint16_t* res,
                  uint16_t* y, int64_t N, int64_t K, float eps, const HeadEpilogue& epi,
                  hipStream_t st) {
   const bool two = EPI || N >= 4 * 2 * 2 * device_cu_count();
   const unsigned grid = (unsigned)(((two ? (N + 1) / 2 : N) + 3) / 4);
-#define LQ_GEMV(RPW, NC)                                                                    \
-  gemv_fused_kernel<RPW, IN, EPI, NC><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N, (int)K, \
-                                                           eps, epi)
+#define LQ_GEMV(RPW, NC, NLM)                                                            \
+  gemv_fused_kernel<RPW, IN, EPI, NC, NLM><<<grid, 256, 0, st>>>(W, x, aux, res, y, (int)N,  \
+                                                                (int)K, eps, epi)
+#define LQ_GEMV_K(RPW)                                 \
+  do {                                                 \
+    if (K == 2048) LQ_GEMV(RPW, 4, 4);                 \
+    else if (K == 4096) LQ_GEMV(RPW, 8, 8);            \
+    else if (K == 6144) LQ_GEMV(RPW, 12, 12);          \
+    else if (K <= 2048) LQ_GEMV(RPW, 0, 4);            \
+    else if (K <= 4096) LQ_GEMV(RPW, 0, 8);            \
+    else LQ_GEMV(RPW, 0, MAXC);                        \
+  } while (0)
   if (two || EPI) {
-    if (K == 2048) LQ_GEMV(2, 4); else if (K == 4096) LQ_GEMV(2, 8); else LQ_GEMV(2, 0);
+    LQ_GEMV_K(2);
   } else if constexpr (!EPI) {
-    if (K == 2048) LQ_GEMV(1, 4); else if (K == 4096) LQ_GEMV(1, 8); else LQ_GEMV(1, 0);
+    LQ_GEMV_K(1);
   }
+#undef LQ_GEMV_K
 #undef LQ_GEMV
 }
 

@@ -153,7 +153,7 @@ def test_attention_block_prefill_decode_verify(dev):
 
 
 @pytest.mark.parametrize("N,K", [(6176, 2048), (2048, 4096), (4608, 4096), (5, 8), (1, 520),
-                                 (4099, 64), (300, 8200)])
+                                 (4099, 64), (300, 8200), (2048, 6144), (129, 7000)])
 def test_gemv_matches_float64(dev, N, K):
     """lq_gemv_bf16 against float64 products of the same bf16 values: within the fp32
     accumulation error plus one bf16 rounding of the result."""
@@ -168,12 +168,14 @@ def test_gemv_matches_float64(dev, N, K):
 
 @pytest.mark.parametrize("mode,per_dim,H,C", [(1, 0, 8, 512), (1, 0, 32, 2048), (2, 0, 8, 512),
                                               (2, 1, 8, 512), (2, 0, 32, 2048), (2, 1, 32, 4608),
-                                              (1, 0, 1, 40)])
+                                              (1, 0, 1, 40), (2, 0, 48, 2048), (2, 1, 56, 1024),
+                                              (1, 0, 48, 6144), (1, 0, 8, 3000)])
 def test_gemv_fused_matches_restatement(dev, mode, per_dim, H, C):
     """lq_gemv_fused: mode 1 = W (RMSNorm(h) w_norm), mode 2 = W (attn * softplus(gate)) plus the
     residual, each against float64 products of the restatement's bf16 input vector (one fp32
-    accumulation and a bf16 rounding or two apart). Widths 2048 and 4096 take the exact-width
-    kernels, the others the bounds-checked one; one and two rows per wave both occur."""
+    accumulation and a bf16 rounding or two apart). Widths 2048, 4096 and 6144 (Laguna's 48-head
+    o_proj) take the exact-width kernels, the others the bounds-checked ones (up to 2048, 4096,
+    8192); one and two rows per wave both occur."""
     from lagunalab_amd import _lib
     rng = np.random.default_rng(50 + mode + per_dim + H + C)
     if mode == 1:
@@ -204,7 +206,7 @@ def test_gemv_fused_matches_restatement(dev, mode, per_dim, H, C):
 
 
 @pytest.mark.parametrize("H,Hkv,C,rot,device_pos", [(32, 8, 2048, 64, False), (32, 8, 2048, 128, True),
-                                                    (4, 2, 520, 0, False)])
+                                                    (4, 2, 520, 0, False), (48, 8, 2048, 64, True)])
 def test_gemv_norm_rope_equals_two_launches(dev, H, Hkv, C, rot, device_pos):
     """lq_gemv_norm_rope = lq_gemv_fused mode 1 followed by lq_qk_norm_rope on the q and k heads,
     bit for bit (the same arithmetic in one launch); a second call with the same counters gives
@@ -244,12 +246,15 @@ def test_gemv_norm_rope_equals_two_launches(dev, H, Hkv, C, rot, device_pos):
 
 @pytest.mark.parametrize("G,B,rot,device_pos,n", [(4, 1, 64, True, 3000), (4, 1, 128, False, 3000),
                                                   (2, 2, 0, True, 3000), (4, 2, 64, False, 3000),
-                                                  (4, 1, 64, True, 7), (1, 1, 128, False, 70)])
+                                                  (4, 1, 64, True, 7), (1, 1, 128, False, 70),
+                                                  (6, 1, 64, True, 3000), (6, 2, 128, False, 3000),
+                                                  (8, 1, 64, True, 70)])
 def test_decode_norm_entry_equals_norm_then_decode(dev, G, B, rot, device_pos, n):
-    """lq_q8_decode_norm_append_attn (q/k RMSNorm + RoPE inside the attention kernel) equals
-    lq_qk_norm_rope followed by the fused decode step, bit for bit: output and cache bytes; host
-    append row or device positions, partial / full / no rotation, one and two sequences, G = 1, 2,
-    4, and short caches where most waves have no super-tile."""
+    """lq_q8_decode_norm_append_attn (q/k RMSNorm + RoPE inside the attention kernel, or for G > 4
+    in a launch of its own before the dense kernel) equals lq_qk_norm_rope followed by the fused
+    decode step, bit for bit: output and cache bytes; host append row or device positions,
+    partial / full / no rotation, one and two sequences, G = 1, 2, 4, 6 (Laguna's 48q/8kv) and 8,
+    and short caches where most waves have no super-tile."""
     from lagunalab_amd import _lib
     from lagunalab_amd.attention import rope_frequencies
     from lagunalab_amd.quant import quantize_kv_into
@@ -345,7 +350,7 @@ def _layers(dev, seed, n0, layers=3, C=512, H=8, Hkv=2, fused=True):
     return blocks, norms, caches
 
 
-@pytest.mark.parametrize("C,H,Hkv", [(512, 8, 2), (2048, 32, 8)])
+@pytest.mark.parametrize("C,H,Hkv", [(512, 8, 2), (2048, 32, 8), (2048, 48, 8)])
 def test_stack_step_matches_restatement(dev, C, H, Hkv):
     """DecodeStack.step (three fused launches per layer) against the float32 restatement of
     each layer: h + o_proj(block(RMSNorm(h) w_norm)) with the reference's bf16 rounding points and
@@ -411,11 +416,13 @@ def test_decode_pos_entry_matches_host_length(dev):
             assert torch.equal(x, y), step
 
 
-def test_graph_step_matches_eager(dev):
+@pytest.mark.parametrize("H,Hkv", [(8, 2), (12, 2)])
+def test_graph_step_matches_eager(dev, H, Hkv):
     """The decode step recorded in a HIP graph (positions on the device) gives the eager step's
     residual stream bit for bit on every replay, with eager GPU work and synchronizations between
-    the replays, and leaves the caches with the same bytes."""
-    a, b = _stack(dev, 41, 4200), _stack(dev, 41, 4200)
+    the replays, and leaves the caches with the same bytes; G = 4 (packed kernel) and G = 6 (norm
+    launch + dense kernel + merge launch)."""
+    a, b = _stack(dev, 41, 4200, H=H, Hkv=Hkv), _stack(dev, 41, 4200, H=H, Hkv=Hkv)
     b.capture(steps=6)
     rng = np.random.default_rng(42)
     for t in range(6):
