@@ -887,7 +887,7 @@ def main():
 
     traffic = None
     tf = ROOT / "profiles" / "q8_decode_traffic.json"
-    if tf.exists() and HQ == 32 and not args.separate_append:
+    if tf.exists() and HQ == 32 and not args.separate_append and ctx == 82671:
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_call")
         except Exception:
