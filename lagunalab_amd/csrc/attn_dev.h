@@ -46,6 +46,14 @@ __device__ __forceinline__ uint32_t pack_h2(float x, float y) {
 
 __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
 
+// One bf16 half of a word as fp32 with one v_perm_b32, the half chosen by a per-lane selector
+// (SEL_LO: bits 0-15, SEL_HI: bits 16-31, moved to the top, zeros below).
+constexpr uint32_t SEL_LO = 0x01000c0cu;
+constexpr uint32_t SEL_HI = 0x03020c0cu;
+__device__ __forceinline__ float bf16_pick(uint32_t w, uint32_t sel) {
+  return __uint_as_float(__builtin_amdgcn_perm(0u, w, sel));
+}
+
 // ---- fp16 operand range. The MFMA operands are fp16 (normal from 2^-14 to 65504, subnormal
 // steps of 2^-24), while the reference computes in fp32 (q8_attn.py:117). Two power-of-two
 // factors keep the operands where fp16 holds them to 11 bits, and come back out exactly:

@@ -7,22 +7,37 @@
 //
 // Work: one workgroup of 8 waves per (sequence, KV head, block of 256 query rows), the rows
 // being PB = 256 / G positions of all G query heads of the KV head; wave w takes 32 rows (two
-// MFMA N tiles of 16) of one head. The workgroup walks the 64-key tiles up to its last row's
-// causal bound (128-key tiles), and each tile is brought into LDS once for all 8 waves:
+// MFMA N tiles of 16) of one head. The workgroup walks the 128-key tiles up to its last row's
+// causal bound; each tile is brought into LDS once for all 8 waves and dequantized once:
 //  * the raw tile (K and V codes, 128 B per key each, and the four bf16 word arrays) is copied
-//    global -> LDS by DMA one tile ahead (two raw slots, 5 copies per thread per tile), landing
-//    while the current tile is dequantized and computed;
-//  * the workgroup dequantizes it once (scale * code + bias in fp32, rounded to fp16) into K [128
-//    keys][128 dims] and V^T [128 dims][128 keys], both XOR-swizzled by 16-byte chunk so that the
-//    MFMA operand reads are conflict-free;
-//  * each wave then runs Q.K^T (v_mfma_f32_16x16x32_f16: M = 16 keys, N = 16 rows, K = 32 dims;
-//    q pre-scaled by scale * log2(e) in fp16), the online softmax with lazy rescaling (a lane
-//    holds keys 16 mt + 4 q + r of one row), and P.V (M = 16 dims, N = 16 rows, K = 32 keys; the
-//    lane's own 8 probabilities are its k-slots: key 32 e + 16 h + 4 q + r of k-step e is slot
-//    8 q + 4 h + r, and V^T stores the keys in that slot order).
-// Tiles past a wave's last row are skipped by that wave; tiles straddling its rows' bounds are
-// masked per row. Rows past L (a ragged last block) read no q and store nothing. Keys past n-1
-// are never read: copies clamp their rows to n-1.
+//    global -> LDS by DMA two tiles ahead (two raw slots, 5 copies per thread per tile);
+//  * the tile is dequantized (scale * code + bias in fp32, rounded to fp16) into K [128 keys][128
+//    dims] and V^T [128 dims][128 keys], both XOR-swizzled by 16-byte chunk so that the MFMA
+//    operand reads are conflict-free;
+//  * each wave runs Q.K^T (v_mfma_f32_16x16x32_f16: M = 16 keys, N = 16 rows, K = 32 dims; q
+//    pre-scaled by scale * log2(e) in fp16; each K fragment read once for both N tiles), the
+//    online softmax with lazy rescaling (a lane holds keys 16 mt + 4 q + r of one row; scores
+//    relative to the running maximum, which the accumulators start from), and P.V (M = 16 dims,
+//    N = 16 rows, K = 32 keys; the lane's own 8 probabilities are its k-slots: key 32 e + 16 h +
+//    4 q + r of k-step e is slot 8 q + 4 h + r, and V^T stores the keys in that slot order).
+// Ping-pong: a SIMD holds one wave of each half of the workgroup (waves 0-3: group A, 4-7: group
+// B), and the two halves run the same per-tile phases one phase apart, so that one wave's matrix
+// phase (Q.K^T or P.V: MFMA and LDS reads) overlaps the other's vector phase (softmax, or its
+// share of the dequantization: K by group A, V by group B). Four barrier-separated slots per tile:
+//
+//   slot    group A                  group B
+//   4t      Q.K^T(t)                 dequantize V(t)
+//   4t+1    softmax(t)               Q.K^T(t)
+//   4t+2    P.V(t)                   softmax(t)
+//   4t+3    dequantize K(t+1)        P.V(t)
+//
+// K(t+1) overwrites K(t) after both halves' Q.K^T(t), V(t) overwrites V(t-1) after both halves'
+// P.V(t-1), so one fp16 K and one V^T buffer suffice. Raw tile t+2 is issued in slot 4t+1 (its
+// slot held raw t, whose K was dequantized in slot 4t-1 and V in slot 4t) and waited for two
+// tiles later.
+// Tiles past a wave's last row are skipped by that wave (it keeps its copy and dequantization
+// duties); tiles straddling its rows' bounds are masked per row. Rows past L (a ragged last block)
+// read no q and store nothing. Keys past n-1 are never read: copies clamp their rows to n-1.
 #include "attn_dev.h"
 
 namespace lq {
@@ -58,6 +73,7 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool grp_a = wv < PW / 2;  // wave-uniform
   const int lc = lane & 15;
   const int lq4 = lane >> 4;
   const int x = blockIdx.x;
@@ -85,6 +101,7 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   const uint32_t lds_raw = lds_addr(&sm.raw[0]);
   const int ck = 16 * wv + (lane >> 3);  // key of this lane's first K / V copy (second: + 8)
   const uint32_t cofs = 16u * (uint32_t)(lane & 7);
+  const uint32_t cofs_v = 16u * (uint32_t)((lane & 7) ^ (lane >> 3));  // V: chunk c of row r at c ^ (r & 7)
   const int wa = wv >> 1;
   const uint16_t* warr = wa == 0 ? ks : wa == 1 ? kb : wa == 2 ? vs : vb;
   const int wkey = 64 * (wv & 1) + lane;
@@ -104,16 +121,102 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
                  :: "v"(kc + kr1 * D + cofs), "s"(mk + 1024u) : "memory");
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :: "v"(vc + kr0 * D + cofs), "s"(mv) : "memory");
+                 :: "v"(vc + kr0 * D + cofs_v), "s"(mv) : "memory");
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :: "v"(vc + kr1 * D + cofs), "s"(mv + 1024u) : "memory");
+                 :: "v"(vc + kr1 * D + cofs_v), "s"(mv + 1024u) : "memory");
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
                  :: "v"(warr + wr * 2), "s"(mw) : "memory");
   };
 
-  issue(0, 0);
+  // ---- dequantization shares: K of a tile by group A (256 threads, 4 chunks of 16 codes each),
+  // V^T by group B (16 slot groups, 4 per wave)
+  const int ta = tid & 255;  // thread index within the group
+  // (the thread index is re-read through an empty asm in each call, so that the compiler
+  // recomputes these addresses in the slot instead of holding them in registers across the loop)
+  auto dequant_k = [&](const PrefillRaw& rw) {
+    int tr = ta;
+    asm volatile("" : "+v"(tr));
+    const int dc = tr & 7;  // 16 codes of key (tr >> 3) + 32 i, dims 16 dc .. 16 dc + 15
+    const uint32_t gsel = (dc >> 2) ? SEL_HI : SEL_LO;
+    uint4 c4[4];
+    uint32_t sw[4], zw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // all reads first: one LDS round trip
+      const int dk = (tr >> 3) + 32 * i;
+      c4[i] = *reinterpret_cast<const uint4*>(rw.k + dk * D + 16 * dc);
+      sw[i] = rw.w[0][dk];
+      zw[i] = rw.w[1][dk];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dk = (tr >> 3) + 32 * i;
+      const float s = bf16_pick(sw[i], gsel);
+      const float z = bf16_pick(zw[i], gsel);
+      const uint32_t cw[4] = {c4[i].x, c4[i].y, c4[i].z, c4[i].w};
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = cw[j];
+        h[2 * j] = pack_h2(fmaf(s, (float)(c & 0xff), z), fmaf(s, (float)((c >> 8) & 0xff), z));
+        h[2 * j + 1] = pack_h2(fmaf(s, (float)((c >> 16) & 0xff), z), fmaf(s, (float)(c >> 24), z));
+      }
+      uint4* kd = reinterpret_cast<uint4*>(sm.k + dk * D);
+      kd[(2 * dc) ^ (dk & 15)] = make_uint4(h[0], h[1], h[2], h[3]);
+      kd[(2 * dc + 1) ^ (dk & 15)] = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+  };
+  // V^T chunk (dim d, k-step e, lane group q) = the 8 keys T[j] = 32 e + 16 (j / 4) + 4 q + j % 4
+  // of dim d, in that slot order. Group B wave e, lane group q: one transposed read
+  // (ds_read_b64_tr_b8) per 16-dim window w gives lane (q, i) the codes of T[0..7] at dim 16 w + i
+  // (source lane s addresses key T[s / 2], bytes 8 (s % 2) of the window; the raw V rows are
+  // stored with 16-byte chunk c of row r at chunk c ^ (r & 7)).
+  auto dequant_v = [&](const PrefillRaw& rw) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int e = wv - PW / 2, qg = ln >> 4, i = ln & 15;
+    const int k0 = 32 * e + 4 * qg;  // T[0..3] = k0 .. k0 + 3, T[4..7] = k0 + 16 .. k0 + 19
+    const int skey = k0 + 16 * (i >> 3) + ((i >> 1) & 3);  // T[i / 2]: this lane's source key
+    const uint8_t* src = rw.v + skey * D + 8 * (i & 1);
+    const int ssw = skey & 7;
+    const uint4 s03 = *reinterpret_cast<const uint4*>(&rw.w[2][k0]);
+    const uint4 s47 = *reinterpret_cast<const uint4*>(&rw.w[2][k0 + 16]);
+    const uint4 z03 = *reinterpret_cast<const uint4*>(&rw.w[3][k0]);
+    const uint4 z47 = *reinterpret_cast<const uint4*>(&rw.w[3][k0 + 16]);
+    const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+    const uint32_t zw[8] = {z03.x, z03.y, z03.z, z03.w, z47.x, z47.y, z47.z, z47.w};
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {  // dims 64 g .. 64 g + 63: quant group g, windows 4 g .. 4 g + 3
+      v2i_t raw[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        raw[w] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(src + 16 * ((4 * g + w) ^ ssw)));
+      float sj[8], zj[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        sj[j] = g ? bf16_hi(sw[j]) : bf16_lo(sw[j]);
+        zj[j] = g ? bf16_hi(zw[j]) : bf16_lo(zw[j]);
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int d = 16 * (4 * g + w) + i;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t word = j < 4 ? (uint32_t)raw[w].x : (uint32_t)raw[w].y;
+          v[j] = fmaf(sj[j], (float)((word >> (8 * (j & 3))) & 0xff), zj[j]);
+        }
+        reinterpret_cast<uint4*>(sm.vt + d * PT)[(4 * e + qg) ^ i] =
+            make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
+                       pack_h2(v[6], v[7]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-  // ---- q of the wave's rows as MFMA B operands, pre-scaled (fp16), while the tile flies
+  issue(0, 0);
+  issue(1, 1);
+
+  // ---- q of the wave's rows as MFMA B operands, pre-scaled (fp16), while the tiles fly
   half8_t qb[2][4];
   int lim[2];  // causal bound of this lane's row per N tile (-1: not a row of the chunk)
 #pragma unroll
@@ -144,129 +247,188 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     lsum[nt] = 0.0f;
   }
 
-  for (int t = 0; t < T; ++t) {
-    const int slot = t & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile t landed
-    __syncthreads();  // every wave's copies of tile t, and every wave done with tile t - 1
-    issue(t + 1, slot ^ 1);  // lands while tile t is dequantized and computed
-    const PrefillRaw& rw = sm.raw[slot];
+  // ---- per-tile phases of one wave
+  // MFMA A fragments: K key 16 mt + lc, dims 32 kk + 8 lq4 .. + 7 at kfrag[kk] + 256 mt (uint4
+  // units); V^T dim 16 dt + lc, slots 32 e + 8 lq4 .. + 7 at vfrag[e] + 256 dt
+  const uint4* kfrag[4];
+  const uint4* vfrag[PE];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {  // K: 16 codes of key dk, dims 16 dc .. 16 dc + 15
-      const int u = tid + 512 * i;
-      const int dk = u >> 3, dc = u & 7;
-      const uint4 c4 = *reinterpret_cast<const uint4*>(rw.k + dk * D + 16 * dc);
-      const int g = dc >> 2;
-      const float s = g ? bf16_hi(rw.w[0][dk]) : bf16_lo(rw.w[0][dk]);
-      const float z = g ? bf16_hi(rw.w[1][dk]) : bf16_lo(rw.w[1][dk]);
-      const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
-      uint32_t h[8];
+  for (int j = 0; j < 4; ++j) {
+    kfrag[j] = reinterpret_cast<const uint4*>(sm.k) + 16 * lc + ((4 * j + lq4) ^ lc);
+    vfrag[j] = reinterpret_cast<const uint4*>(sm.vt) + 16 * lc + ((4 * j + lq4) ^ lc);
+  }
+  f4_t c[2][PMT];     // scores, c[nt][mt]: keys 16 mt + 4 lq4 + r of row 16 nt + lc (log2 units)
+  half8_t pw[2][PE];  // P in fp16, per N tile and k-step
+  // Q.K^T of both N tiles from one read of each K fragment, relative to the rows' running
+  // maxima (0 before the first): the accumulators start at -mref
+  auto qk = [&]() {
+    float mref[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t c = cw[j];
-        h[2 * j] = pack_h2(fmaf(s, (float)(c & 0xff), z), fmaf(s, (float)((c >> 8) & 0xff), z));
-        h[2 * j + 1] = pack_h2(fmaf(s, (float)((c >> 16) & 0xff), z), fmaf(s, (float)(c >> 24), z));
+    for (int nt = 0; nt < 2; ++nt) mref[nt] = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+    // fragments one M tile ahead of the MFMAs that use them (the scheduling barriers keep the
+    // reads of M tile mt + 1 issued before the MFMAs of M tile mt)
+    uint4 fa[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) fa[0][kk] = kfrag[kk][0];
+#pragma unroll
+    for (int mt = 0; mt < PMT; ++mt) {
+      if (mt + 1 < PMT) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) fa[(mt + 1) & 1][kk] = kfrag[kk][256 * (mt + 1)];
       }
-      uint4* kd = reinterpret_cast<uint4*>(sm.k + dk * D);
-      kd[(2 * dc) ^ (dk & 15)] = make_uint4(h[0], h[1], h[2], h[3]);
-      kd[(2 * dc + 1) ^ (dk & 15)] = make_uint4(h[4], h[5], h[6], h[7]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) c[nt][mt] = f4_t{-mref[nt], -mref[nt], -mref[nt], -mref[nt]};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint4 a = fa[mt & 1][kk];  // key 16 mt + lc
+        const half8_t ah = words_as_h8(a.x, a.y, a.z, a.w);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          c[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qb[nt][kk], c[nt][mt], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {  // V: slot group wv + 8 i (k-step ve, lane group vq), dims 2 lane, +1
-      const int grp = wv + 8 * i;
-      const int ve = grp >> 2, vq = grp & 3;
-      const int g = lane >> 5;
-      float lo[8], hi[8];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = 32 * ve + 16 * hh + 4 * vq + r;
-          const uint32_t c2 = *reinterpret_cast<const uint16_t*>(rw.v + key * D + 2 * lane);
-          const float s = g ? bf16_hi(rw.w[2][key]) : bf16_lo(rw.w[2][key]);
-          const float z = g ? bf16_hi(rw.w[3][key]) : bf16_lo(rw.w[3][key]);
-          lo[4 * hh + r] = fmaf(s, (float)(c2 & 0xff), z);
-          hi[4 * hh + r] = fmaf(s, (float)(c2 >> 8), z);
-        }
-      const int d0 = 2 * lane;
-      const int chunk = 4 * ve + vq;  // slots 32 ve + 8 vq .. + 7
-      reinterpret_cast<uint4*>(sm.vt + d0 * PT)[chunk ^ (d0 & 15)] =
-          make_uint4(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]), pack_h2(lo[4], lo[5]),
-                     pack_h2(lo[6], lo[7]));
-      reinterpret_cast<uint4*>(sm.vt + (d0 + 1) * PT)[chunk ^ ((d0 + 1) & 15)] =
-          make_uint4(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]), pack_h2(hi[4], hi[5]),
-                     pack_h2(hi[6], hi[7]));
-    }
-    __syncthreads();
-
-    const int t0 = PT * t;
-    if (t0 > lim_hi) continue;  // wave-uniform: no key of this tile is visible to its rows
-    const bool full = t0 + PT - 1 <= lim_lo;
-
-    // Per N tile: Q.K^T, softmax, P.V. The N tiles' chains are independent, so the second
-    // tile's MFMAs can run while the first tile's softmax (VALU, exp) issues.
-    // c: keys 16 mt + 4 lq4 + r of row 16 nt + lc (log2 units)
+  };
+  // softmax per N tile: masking, lazy rescale, P in fp16 and the row sum of those same fp16
+  // values (v_dot2_f32_f16 against ones)
+  auto softmax = [&](int t0, bool full) {
+    const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      f4_t c[PMT];
-#pragma unroll
-      for (int mt = 0; mt < PMT; ++mt) {
-        const int key = 16 * mt + lc;
-        const uint4* kr = reinterpret_cast<const uint4*>(sm.k + key * D);
-        c[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const uint4 a = kr[(4 * kk + lq4) ^ lc];
-          c[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(words_as_h8(a.x, a.y, a.z, a.w),
-                                                         qb[nt][kk], c[mt], 0, 0, 0);
-        }
-      }
       if (!full) {
 #pragma unroll
         for (int mt = 0; mt < PMT; ++mt)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            c[mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? c[mt][r] : -INFINITY;
+            c[nt][mt][r] = t0 + 16 * mt + 4 * lq4 + r <= lim[nt] ? c[nt][mt][r] : -INFINITY;
       }
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < PMT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, c[mt][r]);
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, c[nt][mt][r]);
       tmax = max_xor16(tmax);
       tmax = max_xor32(tmax);
-      const bool bump = tmax > m_run[nt] + RESCALE_LOG2;
+      // a new running maximum: the tile's exceeds it by more than RESCALE_LOG2 (any finite one
+      // the first time)
+      const bool bump = tmax > (m_run[nt] == -INFINITY ? -INFINITY : RESCALE_LOG2);
       if (__builtin_amdgcn_ballot_w64(bump)) {
-        const float mn = bump ? tmax : m_run[nt];
+        const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+        const float mn = bump ? mref + tmax : m_run[nt];
         const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
         m_run[nt] = mn;
         lsum[nt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+        const float shift = bump ? tmax : 0.0f;  // new reference minus the one the scores hold
+#pragma unroll
+        for (int mt = 0; mt < PMT; ++mt) c[nt][mt] -= shift;
       }
-      const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float ls = 0.0f;
 #pragma unroll
       for (int e = 0; e < PE; ++e) {
-        float p[8];
+        half2_t ph[4];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[4 * hh + r] = __builtin_amdgcn_exp2f(c[2 * e + hh][r] - mref);
-            ls += p[4 * hh + r];
-          }
-        const half8_t pb = words_as_h8(pack_h2(p[0], p[1]), pack_h2(p[2], p[3]),
-                                       pack_h2(p[4], p[5]), pack_h2(p[6], p[7]));
-        // P.V: out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int d = 16 * dt + lc;
-          const uint4 a = reinterpret_cast<const uint4*>(sm.vt + d * PT)[(4 * e + lq4) ^ (d & 15)];
-          oacc[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(words_as_h8(a.x, a.y, a.z, a.w),
-                                                                pb, oacc[nt][dt], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+          const int hh = j >> 1, r = 2 * (j & 1);
+          ph[j] = half2_t{(_Float16)__builtin_amdgcn_exp2f(c[nt][2 * e + hh][r]),
+                          (_Float16)__builtin_amdgcn_exp2f(c[nt][2 * e + hh][r + 1])};
+          ls = __builtin_amdgcn_fdot2(ph[j], ones, ls, false);
         }
+        pw[nt][e] = __builtin_bit_cast(half8_t, ph);
       }
       lsum[nt] += ls;
+    }
+  };
+  // P.V of both N tiles from one read of each V^T fragment:
+  // out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
+  auto pv = [&]() {
+    // fragments four dims tiles ahead (half a k-step), as in qk: step u = (k-step u / 2, dim
+    // tiles 4 (u % 2) .. + 3)
+    uint4 fv[2][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fv[0][j] = vfrag[0][256 * j];
+#pragma unroll
+    for (int u = 0; u < 2 * PE; ++u) {
+      if (u + 1 < 2 * PE) {
+        const int e1 = (u + 1) >> 1, d1 = 4 * ((u + 1) & 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fv[(u + 1) & 1][j] = vfrag[e1][256 * (d1 + j)];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int e = u >> 1, d0 = 4 * (u & 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 a = fv[u & 1][j];  // dim 16 (d0 + j) + lc
+        const half8_t ah = words_as_h8(a.x, a.y, a.z, a.w);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          oacc[nt][d0 + j] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, pw[nt][e], oacc[nt][d0 + j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- prologue: raw tile 0 landed (only tile 1's copies outstanding), K(0) dequantized
+  asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  __syncthreads();
+  if (grp_a) dequant_k(sm.raw[0]);
+  __syncthreads();
+
+  // The two halves run their own loops (wave-uniform branch): each wave passes the same four
+  // barriers per tile. Tiles 0 .. Tact - 1 hold keys visible to the wave's rows; past them the
+  // wave keeps only its copy and dequantization duties. (Two loops rather than a condition per
+  // phase, so that the scores and P are not live across the loop's back edge.)
+  const int Tact = lim_hi < 0 ? 0 : min(T, lim_hi / PT + 1);
+  if (grp_a) {
+    int t = 0;
+    for (; t < Tact; ++t) {
+      const int t0 = PT * t;
+      qk();                                            // slot 4t
+      __syncthreads();
+      issue(t + 2, t & 1);                             // slot 4t + 1: raw t + 2 into t's slot
+      softmax(t0, t0 + PT - 1 <= lim_lo);
+      __syncthreads();
+      pv();                                            // slot 4t + 2
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // raw tile t + 1 landed
+      __syncthreads();
+      if (t + 1 < T) dequant_k(sm.raw[(t + 1) & 1]);  // slot 4t + 3
+      __syncthreads();
+    }
+    for (; t < T; ++t) {
+      __syncthreads();
+      issue(t + 2, t & 1);
+      __syncthreads();
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      __syncthreads();
+      if (t + 1 < T) dequant_k(sm.raw[(t + 1) & 1]);
+      __syncthreads();
+    }
+  } else {
+    int t = 0;
+    for (; t < Tact; ++t) {
+      const int t0 = PT * t;
+      dequant_v(sm.raw[t & 1]);                        // slot 4t
+      __syncthreads();
+      issue(t + 2, t & 1);                             // slot 4t + 1
+      qk();
+      __syncthreads();
+      softmax(t0, t0 + PT - 1 <= lim_lo);              // slot 4t + 2
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      __syncthreads();
+      pv();                                            // slot 4t + 3
+      __syncthreads();
+    }
+    for (; t < T; ++t) {
+      dequant_v(sm.raw[t & 1]);
+      __syncthreads();
+      issue(t + 2, t & 1);
+      __syncthreads();
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      __syncthreads();
+      __syncthreads();
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end
