@@ -45,6 +45,14 @@ namespace {
 
 using namespace attn;
 
+// Codes 2 h, 2 h + 1 of a word as the fp16 pair 1024 + c (exponent 10: the code is the mantissa),
+// one v_perm_b32; scale * (1024 + c) + (bias - 1024 scale) then dequantizes in one
+// v_fma_mix (fp32 arithmetic, rounded once to fp16).
+__device__ __forceinline__ half2_t codes_1024(uint32_t w, int h) {
+  return __builtin_bit_cast(half2_t,
+                            __builtin_amdgcn_perm(0x64646464u, w, h ? 0x04030402u : 0x04010400u));
+}
+
 constexpr int PW = 8;       // waves per workgroup
 constexpr int PROWS = 256;  // query rows per workgroup
 constexpr int PT = 128;     // keys per tile
@@ -151,14 +159,14 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
     for (int i = 0; i < 4; ++i) {
       const int dk = (tr >> 3) + 32 * i;
       const float s = bf16_pick(sw[i], gsel);
-      const float z = bf16_pick(zw[i], gsel);
+      const float z = fmaf(-1024.0f, s, bf16_pick(zw[i], gsel));  // bias - 1024 scale
       const uint32_t cw[4] = {c4[i].x, c4[i].y, c4[i].z, c4[i].w};
       uint32_t h[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t c = cw[j];
-        h[2 * j] = pack_h2(fmaf(s, (float)(c & 0xff), z), fmaf(s, (float)((c >> 8) & 0xff), z));
-        h[2 * j + 1] = pack_h2(fmaf(s, (float)((c >> 16) & 0xff), z), fmaf(s, (float)(c >> 24), z));
+        const half2_t c01 = codes_1024(cw[j], 0), c23 = codes_1024(cw[j], 1);
+        h[2 * j] = pack_h2(fmaf(s, (float)c01.x, z), fmaf(s, (float)c01.y, z));
+        h[2 * j + 1] = pack_h2(fmaf(s, (float)c23.x, z), fmaf(s, (float)c23.y, z));
       }
       uint4* kd = reinterpret_cast<uint4*>(sm.k + dk * D);
       kd[(2 * dc) ^ (dk & 15)] = make_uint4(h[0], h[1], h[2], h[3]);
@@ -190,20 +198,24 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
 #pragma unroll
       for (int w = 0; w < 4; ++w)
         raw[w] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(src + 16 * ((4 * g + w) ^ ssw)));
-      float sj[8], zj[8];
+      float sj[8], zj[8];  // scale and bias - 1024 scale of key T[j], group g
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         sj[j] = g ? bf16_hi(sw[j]) : bf16_lo(sw[j]);
-        zj[j] = g ? bf16_hi(zw[j]) : bf16_lo(zw[j]);
+        zj[j] = fmaf(-1024.0f, sj[j], g ? bf16_hi(zw[j]) : bf16_lo(zw[j]));
       }
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int d = 16 * (4 * g + w) + i;
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t word = j < 4 ? (uint32_t)raw[w].x : (uint32_t)raw[w].y;
-          v[j] = fmaf(sj[j], (float)((word >> (8 * (j & 3))) & 0xff), zj[j]);
+        for (int hw = 0; hw < 2; ++hw) {  // keys T[4 hw .. 4 hw + 3]
+          const uint32_t word = hw ? (uint32_t)raw[w].y : (uint32_t)raw[w].x;
+          const half2_t c01 = codes_1024(word, 0), c23 = codes_1024(word, 1);
+          v[4 * hw + 0] = fmaf(sj[4 * hw + 0], (float)c01.x, zj[4 * hw + 0]);
+          v[4 * hw + 1] = fmaf(sj[4 * hw + 1], (float)c01.y, zj[4 * hw + 1]);
+          v[4 * hw + 2] = fmaf(sj[4 * hw + 2], (float)c23.x, zj[4 * hw + 2]);
+          v[4 * hw + 3] = fmaf(sj[4 * hw + 3], (float)c23.y, zj[4 * hw + 3]);
         }
         reinterpret_cast<uint4*>(sm.vt + d * PT)[(4 * e + qg) ^ i] =
             make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
@@ -238,14 +250,18 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   }
 
   f4_t oacc[2][8];
-  float m_run[2], lsum[2];
+  f4_t lacc[2];  // row sums of P (MFMA layout: all four values of a lane hold its row's sum)
+  float m_run[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    lacc[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     m_run[nt] = -INFINITY;
-    lsum[nt] = 0.0f;
   }
+  half8_t ones8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones8[j] = (_Float16)1.0f;
 
   // ---- per-tile phases of one wave
   // MFMA A fragments: K key 16 mt + lc, dims 32 kk + 8 lq4 .. + 7 at kfrag[kk] + 256 mt (uint4
@@ -262,9 +278,12 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   // Q.K^T of both N tiles from one read of each K fragment, relative to the rows' running
   // maxima (0 before the first): the accumulators start at -mref
   auto qk = [&]() {
-    float mref[2];
+    f4_t cinit[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) mref[nt] = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+    for (int nt = 0; nt < 2; ++nt) {
+      const float mref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+      cinit[nt] = f4_t{-mref, -mref, -mref, -mref};
+    }
     // fragments one M tile ahead of the MFMAs that use them (the scheduling barriers keep the
     // reads of M tile mt + 1 issued before the MFMAs of M tile mt)
     uint4 fa[2][4];
@@ -278,22 +297,19 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) c[nt][mt] = f4_t{-mref[nt], -mref[nt], -mref[nt], -mref[nt]};
-#pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const uint4 a = fa[mt & 1][kk];  // key 16 mt + lc
         const half8_t ah = words_as_h8(a.x, a.y, a.z, a.w);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          c[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qb[nt][kk], c[nt][mt], 0, 0, 0);
+        for (int nt = 0; nt < 2; ++nt)  // each chain starts from the shared -mref tuple
+          c[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qb[nt][kk],
+                                                             kk == 0 ? cinit[nt] : c[nt][mt], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // softmax per N tile: masking, lazy rescale, P in fp16 and the row sum of those same fp16
-  // values (v_dot2_f32_f16 against ones)
+  // softmax per N tile: masking, lazy rescale, P in fp16 (its row sums are taken by P.V)
   auto softmax = [&](int t0, bool full) {
-    const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       if (!full) {
@@ -318,14 +334,13 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
         const float mn = bump ? mref + tmax : m_run[nt];
         const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
         m_run[nt] = mn;
-        lsum[nt] *= alpha;
+        lacc[nt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
         const float shift = bump ? tmax : 0.0f;  // new reference minus the one the scores hold
 #pragma unroll
         for (int mt = 0; mt < PMT; ++mt) c[nt][mt] -= shift;
       }
-      float ls = 0.0f;
 #pragma unroll
       for (int e = 0; e < PE; ++e) {
         half2_t ph[4];
@@ -334,14 +349,12 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
           const int hh = j >> 1, r = 2 * (j & 1);
           ph[j] = half2_t{(_Float16)__builtin_amdgcn_exp2f(c[nt][2 * e + hh][r]),
                           (_Float16)__builtin_amdgcn_exp2f(c[nt][2 * e + hh][r + 1])};
-          ls = __builtin_amdgcn_fdot2(ph[j], ones, ls, false);
         }
         pw[nt][e] = __builtin_bit_cast(half8_t, ph);
       }
-      lsum[nt] += ls;
     }
   };
-  // P.V of both N tiles from one read of each V^T fragment:
+  // P.V of both N tiles from one read of each V^T fragment, and the rows' sums of P:
   // out^T[16 dt + 4 lq4 + r][row 16 nt + lc] += V^T[dims][slots] P^T[slots][rows]
   auto pv = [&]() {
     // fragments four dims tiles ahead (half a k-step), as in qk: step u = (k-step u / 2, dim
@@ -358,6 +371,11 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       const int e = u >> 1, d0 = 4 * (u & 1);
+      if (u & 1) {  // row sums of this k-step's P: a ones A operand (every output row the sum)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          lacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones8, pw[nt][e], lacc[nt], 0, 0, 0);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint4 a = fv[u & 1][j];  // dim 16 (d0 + j) + lc
@@ -433,10 +451,10 @@ __global__ __launch_bounds__(64 * PW, 1) void q8_prefill_kernel(
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end
 
-  // ---- output rows: acc / l (the row's partial sums of its four lane groups added)
+  // ---- output rows: acc / l
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    float l = sum_xor32(sum_xor16(lsum[nt]));
+    const float l = lacc[nt][0];
     const int i = p0 + 16 * nt + lc;
     if (lim[nt] < 0) continue;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
