@@ -94,7 +94,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   int b;
   find_seq(plan, x, b);
   const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap) : plan.len[b];
-  // Work in super-tiles of PST keys. The NWS waves of the sequence's workgroups take about 80%
+  // Work in super-tiles of PST keys. The NWS waves of the sequence's workgroups take about 90%
   // of them statically (wave gw: super-tiles gw + k NWS for k < NS), the rest one at a time from
   // the (sequence, KV head) tile counter, two super-tiles ahead. Waves that started late or sit
   // on busier parts of the chip (XCDs start up to ~3 us apart and differ by ~10% in the
@@ -102,7 +102,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   const int T = (n + PST - 1) / PST;
   const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * NWAVE;
   const int gw = (x - plan.split_begin[b]) * NWAVE + wv;
-  const int NS = max(2, (4 * T) / (5 * NWS));  // static super-tiles per wave
+  const int NS = max(2, (9 * T) / (10 * NWS));  // static super-tiles per wave
   const int R = G * L;  // <= 4
   // Fused append: the wave that gets super-tile app_t (holding row n - 1, the sequence's new last
   // row) patches the new K and V rows, quantized by every wave up front, into its LDS copy of that
