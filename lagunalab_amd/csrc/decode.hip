@@ -18,7 +18,7 @@
 namespace lq {
 namespace {
 
-constexpr int MIN_CHUNK = 128;
+constexpr int MIN_CHUNK = 256;  // keys per split at least (4,096 keys: 16 splits per head)
 constexpr int64_t MAX_SPLITS = 32;    // kernels that merge their own splits (merge_rows4)
 constexpr int64_t MERGE_SPLITS = 64;  // kernels whose splits decode_merge_kernel merges
 

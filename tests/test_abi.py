@@ -139,6 +139,6 @@ def test_decode_split_plan_fills_one_wave(lib):
     c3 = [int(x) for x in np.random.default_rng(1).integers(42771, 82672, size=8)]
     assert splits(c3) == 32
     assert splits([82671]) == 32
-    assert splits([1000]) == 8        # at least 128 keys per split
+    assert splits([1000]) == 4        # at least 256 keys per split
     assert splits([1, 1, 1]) == 3     # one split per sequence at least
     assert splits([5000] * 40) == 40  # more sequences than the budget: one split each
