@@ -1,5 +1,6 @@
-// Attention over the 8-bit KV cache for more than 4 query rows per KV head: the causal verify
-// block of speculative decoding (G * L rows, L <= 16) and single-token decode with G > 4.
+// Attention over the 8-bit KV cache for more than 4 query rows per KV head -- the causal verify
+// block of speculative decoding (G * L rows, L <= 16) and single-token decode with G > 4 -- and
+// for up to 4 rows over a single sequence of at most 65,536 rows.
 //
 // Replaces, for verify blocks, the reference's unfused path (dequantize, laguna_mlx/cache.py:
 // 99-100, then SDPA with the bottom-right causal mask, laguna.py:107, 183-186), and for decode

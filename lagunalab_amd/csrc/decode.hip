@@ -181,7 +181,15 @@ void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq
                                                               plan, out);
 }
 
-bool attn_merges_itself(int64_t rows_per_kv_head) { return rows_per_kv_head <= 4; }
+// 8-bit cache, at most 4 query rows per KV head: the packed kernel (in-kernel split merge) unless
+// there is one sequence of at most DENSE_BELOW rows, where the dense kernel on 32-key
+// super-tiles with 8 waves per workgroup and a merge launch is faster (µs per decode step,
+// 32q/8kv: 1,024 keys 12.1 -> 11.6, 4,096 13.4 -> 12.2, 16,384 18.5 -> 16.3, 32,768 22.8 -> 20.9;
+// at 82,671 both 37.5; a ragged batch of 8 long sequences 182.8 -> 193.5, so not there).
+constexpr int64_t DENSE_BELOW = 65536;
+bool q8_packed(int64_t R, int64_t B, int64_t longest) {
+  return R <= 4 && !(B == 1 && longest <= DENSE_BELOW);
+}
 
 // Decode with the dense kernel: where the q and new K rows after q/k norm + RoPE go in the
 // workspace (behind the partials, 256-byte aligned).
@@ -192,29 +200,34 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
                   const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
                   int64_t& ws_bytes) {
   const int64_t R = (Hq / Hkv) * L;
+  if (B < 1 || B > LQ_MAX_SEQS) return -1;
+  int64_t longest = n;
+  if (lens) {
+    longest = 0;
+    for (int64_t b = 0; b < B; ++b) longest = std::max<int64_t>(longest, lens[b]);
+  }
   if (kind == LQ_KV_Q8) {
     const int nt = (int)((R + 15) / 16);
-    if (attn_merges_itself(R))
-      k = {q8_attn_fn(L > 1), 256};
+    if (q8_packed(R, B, longest))
+      k = {q8_attn_fn(L > 1), 256, true};
     else
-      k = {q8_dense_attn_fn(nt, L > 1), q8_dense_threads(nt)};
+      k = {q8_dense_attn_fn(nt, L > 1), q8_dense_threads(nt), false};
   } else if (kind == LQ_KV_BF16 && R <= 4) {
-    k = {bf16_attn_fn(L > 1), 128};
+    k = {bf16_attn_fn(L > 1), 128, true};
   } else if (kind == LQ_KV_Q4 && R <= 4) {
-    k = {q4_attn_fn(L > 1), 256};
+    k = {q4_attn_fn(L > 1), 256, true};
   } else {
     return -1;
   }
   if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
   // One workgroup per CU for the dense kernel too (its 8 or 4 waves hold about 150 KB of LDS).
-  const int per_cu = attn_merges_itself(R) || kind != LQ_KV_Q8 ? attn_occupancy(k.fn, k.threads) : 1;
+  const int per_cu = k.merges ? attn_occupancy(k.fn, k.threads) : 1;
   const int64_t S = make_plan(B, Hkv, n, lens, cap, per_cu * device_cu_count(),
-                              kind == LQ_KV_Q8, attn_merges_itself(R) ? MAX_SPLITS : MERGE_SPLITS,
-                              plan);
+                              kind == LQ_KV_Q8, k.merges ? MAX_SPLITS : MERGE_SPLITS, plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
-  if (kind == LQ_KV_Q8 && L == 1 && !attn_merges_itself(R))  // normalized q / k rows (norm entry)
+  if (kind == LQ_KV_Q8 && L == 1 && !k.merges)  // normalized q / k rows (norm entry)
     ws_bytes = norm_rows_offset(ws_bytes) + B * (Hq + Hkv) * D * (int64_t)sizeof(uint16_t);
   return S;
 }
@@ -278,7 +291,7 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  const bool fused_merge = kind != LQ_KV_Q8 || attn_merges_itself(Hq / Hkv);
+  const bool fused_merge = kern.merges;
   LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new),
                "device positions need the fused 8-bit append");
   LQ_CHECK_ARG(!norm || (kind == LQ_KV_Q8 && k_new), "the q/k norm needs the fused 8-bit append");

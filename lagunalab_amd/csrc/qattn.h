@@ -94,6 +94,7 @@ int q8_dense_threads(int nt);
 struct AttnKernel {
   QAttnFn fn;
   int threads;
+  bool merges;  // the kernel merges the split partials itself (else decode_merge_kernel does)
 };
 
 // Plain-bf16 cache kernel (attn_bf16.hip), G * L <= 4.
@@ -108,9 +109,6 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
                   const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
                   int64_t& ws_bytes);
 
-// True when the attention kernel for this many query rows per KV head (G * L) merges the
-// split partials itself (the packed kernel).
-bool attn_merges_itself(int64_t rows_per_kv_head);
 
 // Per-sequence log-sum-exp merge of split partials: rows_per_seq = Hq * L partial rows per split.
 void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq,

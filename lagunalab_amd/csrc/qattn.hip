@@ -1,6 +1,7 @@
 // Fused attention over the 8-bit KV cache on MFMA for at most 4 query rows per KV head:
-// single-token decode with G <= 4 and small causal verify blocks (G * L <= 4). Larger blocks take
-// the dense-layout kernel (attn_dense.hip).
+// single-token decode with G <= 4 and small causal verify blocks (G * L <= 4), over batches or
+// over a single sequence of more than 65,536 rows. Larger blocks, and shorter single sequences,
+// take the dense-layout kernel (attn_dense.hip).
 //
 // Replaces q8_decode_attention (laguna_mlx/q8_attn.py:102-130: the Metal kernel at :17-99 and the
 // block merge at :126-130) and, for verify blocks, the reference's unfused path (dequantize,

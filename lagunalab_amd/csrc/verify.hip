@@ -4,8 +4,8 @@
 // (laguna_mlx/dflash.py:195) over DequantKVCache's dequantized K/V (cache.py:99-100) with the
 // bottom-right causal mask (laguna.py:107, 183-186): the L query rows of each head are the
 // block's own last L keys, and row i sees keys 0 .. n-L+i. G*L <= 4 rows per KV head take the
-// packed decode kernel (qattn.hip), larger blocks the dense kernel (attn_dense.hip), with the
-// causal bound applied per query row.
+// packed decode kernel (qattn.hip) -- except a single sequence of at most 65,536 rows --, the
+// rest the dense kernel (attn_dense.hip), with the causal bound applied per query row.
 #include "common.h"
 #include "qattn.h"
 
@@ -59,7 +59,7 @@ int verify_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  const bool packed = attn_merges_itself((Hq / Hkv) * L);
+  const bool packed = kern.merges;
   AttnArgs a{};
   a.q = q;
   a.kc = kc;

@@ -178,23 +178,24 @@ def test_decode_matches_unfused_oracle(dev, n, G, B):
     assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale), f"unfused n={n} G={G}", at, rt)
 
 
-@pytest.mark.parametrize("n", [16500, 18000, 20400])
+@pytest.mark.parametrize("n", [8500, 11000, 13500])
 def test_decode_two_static_super_tiles(dev, n):
-    """One sequence, 8 KV heads: 128 waves share the keys; between about 16.3k and 20.5k keys
-    each wave takes two super-tiles statically and its third from the tile counter (its first
-    dynamic one), so the counter must be read already for that third super-tile."""
+    """The packed kernel (two sequences, so that short lengths take it too), 8 KV heads: each
+    sequence's 16 workgroups give 64 waves; between about 8.2k and 13.6k keys each wave takes two
+    super-tiles statically and its third from the tile counter (its first dynamic one), so the
+    counter must be read already for that third super-tile."""
     from lagunalab_amd.q8_attn import decode_append_attention, q8_decode_attention
     rng = np.random.default_rng(n)
-    Hkv, G = 8, 4
+    Hkv, G, B = 8, 4, 2
     cap = (n + 256) // 256 * 256
-    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
-    q = Q.randn_bf16(rng, (1, Hkv * G, 1, 128))
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (B, Hkv * G, 1, 128))
     got = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, n, 0.09)
     kn, vn = cache_np(kq), cache_np(vq)
     assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"decode n={n}")
     # the fused step at the same length: append row n - 1, attend over n rows
-    k1 = to_dev_bf16(Q.randn_bf16(rng, (1, Hkv, 1, 128)), dev)
-    v1 = to_dev_bf16(Q.randn_bf16(rng, (1, Hkv, 1, 128)), dev)
+    k1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    v1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
     got = decode_append_attention(to_dev_bf16(q, dev), k1, v1, kq, vq, n=n - 1, scale=0.09)
     kn, vn = cache_np(kq), cache_np(vq)
     assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"fused step n={n}")
@@ -647,6 +648,25 @@ def test_verify_matches_causal_oracle(dev, n, L, G):
     at, rt = unfused_tol(n)
     assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale, causal=True),
                       f"unfused verify n={n} L={L} G={G}", at, rt)
+
+
+@pytest.mark.parametrize("n,L,G", [(1500, 4, 1), (900, 2, 2), (130, 3, 1), (70000, 2, 2)])
+def test_verify_packed_kernel_matches_causal_oracle(dev, n, L, G):
+    """G * L <= 4 rows per KV head over two sequences, or one of more than 65,536 rows: the
+    packed kernel's causal variant (a single shorter sequence takes the dense kernel, which the
+    test above covers)."""
+    from lagunalab_amd.q8_attn import q8_verify_attention
+    rng = np.random.default_rng(n + 3 * L + G)
+    Hkv = 8
+    B = 1 if n > 65536 else 2
+    cap = (n + 255) // 256 * 256
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (B, Hkv * G, L, 128))
+    scale = 128 ** -0.5
+    got = q8_verify_attention(to_dev_bf16(q, dev), kq, vq, n, scale)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, scale, causal=True),
+                      f"fused verify n={n} L={L} G={G} B={B}")
 
 
 @pytest.mark.parametrize("n,L,G,B", [(0, 5, 4, 1), (100, 5, 4, 1), (4093, 5, 4, 1), (65536, 5, 4, 1),
