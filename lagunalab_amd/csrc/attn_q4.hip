@@ -8,9 +8,13 @@
 //    the whole workgroup needs 80 KB of LDS, so two workgroups share a CU.
 //  * Rows are 64 bytes; chunk c of row r sits at chunk position c ^ ((r >> 2) & 3), which puts
 //    the 16 rows read together in 16 different bank quarters.
-//  * Codes become fp16 subnormals c * 2^-24 after splitting the nibbles (and, shift, and):
-//    one 32-bit word of K (8 dims) is one MFMA step; one ds_read_b64_tr_b8 of V gives every lane
-//    8 keys of two adjacent dims, i.e. two A operands (even and odd dims).
+//  * Codes become fp16 subnormals by masking: a 16-bit half keeps one nibble, at c * 2^-24 (low
+//    nibble) or 16 c * 2^-24 (high nibble), so 8 codes take 5 operations (two masks of the word,
+//    one shift, two masks of the shifted word) and come out in the k-slot order {0, 4, 1, 5, 2, 6,
+//    3, 7}. One 32-bit word of K (8 dims) is one MFMA step; the q operands follow that order with
+//    1/16 on the high-nibble slots. One ds_read_b64_tr_b8 of V gives every lane 8 keys of two
+//    adjacent dims, i.e. two A operands (even dims at 2^-24, odd dims at 16 * 2^-24: their
+//    accumulators are scaled by 1/16 at the end), with the P operand in the same key order.
 #include "attn_dev.h"
 
 namespace lq {
@@ -22,7 +26,6 @@ constexpr int QW = 4;
 constexpr int QTHR = 64 * QW;
 constexpr int QPST = 64;
 constexpr int QROW = D / 2;  // bytes per 4-bit row
-constexpr uint32_t NIB = 0x0f0f0f0fu;
 
 struct Q4Buf {
   uint8_t k[QPST * QROW];
@@ -52,12 +55,16 @@ struct Q4Smem {
   };
 };
 
-// 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals.
+// 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals, in the
+// k-slot order {0, 4, 1, 5, 2, 6, 3, 7}: masks keep two nibbles per word, one in each half, so
+// that each 16-bit half holds one code. Low nibbles land at c * 2^-24, high nibbles (bits 4-7 of a
+// half) at 16 c * 2^-24; the other operand carries 1/16 for those slots. Five operations per eight
+// codes.
+constexpr uint32_t NIB_LO = 0x000f000fu, NIB_HI = 0x00f000f0u;
 __device__ __forceinline__ half8_t nib8_sub(uint32_t w) {
-  const uint32_t lo = w & NIB, hi = (w >> 4) & NIB;
+  const uint32_t w8 = w >> 8;
   typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
-  const u4v_t u = {__builtin_amdgcn_perm(hi, lo, 0x0c040c00u), __builtin_amdgcn_perm(hi, lo, 0x0c050c01u),
-                   __builtin_amdgcn_perm(hi, lo, 0x0c060c02u), __builtin_amdgcn_perm(hi, lo, 0x0c070c03u)};
+  const u4v_t u = {w & NIB_LO, w & NIB_HI, w8 & NIB_LO, w8 & NIB_HI};
   return __builtin_bit_cast(half8_t, u);
 }
 
@@ -222,20 +229,20 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     const float ks0v[4] = {ks0.x, ks0.y, ks0.z, ks0.w}, ks1v[4] = {ks1.x, ks1.y, ks1.z, ks1.w};
     const float ku0v[4] = {ku0.x, ku0.y, ku0.z, ku0.w}, ku1v[4] = {ku1.x, ku1.y, ku1.z, ku1.w};
     float sc[4];
-    float tmax = -INFINITY;
     const bool full = t0 + QPST <= w_end && (!CAUSAL || t0 + QPST - 1 <= n - L);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = fmaf(ks0v[r], c0[r], fmaf(ks1v[r], c1[r], fmaf(ku1v[r], qsum[1], ku0v[r] * qsum[0])));
-      if (!full) {
+    for (int r = 0; r < 4; ++r)
+      sc[r] = fmaf(ks0v[r], c0[r], fmaf(ks1v[r], c1[r], fmaf(ku1v[r], qsum[1], ku0v[r] * qsum[0])));
+    if (!full) {  // keys past the wave's range or the row's causal bound (last super-tile only)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
         const int t = t0 + k0 + r;
         bool ok = t < w_end;
         if (CAUSAL) ok = ok && t <= causal_bound;
-        v = ok ? v : -INFINITY;
+        sc[r] = ok ? sc[r] : -INFINITY;
       }
-      sc[r] = v;
-      tmax = fmaxf(tmax, v);
     }
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
     tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
     tmax = max_xor16(tmax);
@@ -278,10 +285,11 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
       bsum0 = fmaf(p[r], vb0v[r], bsum0);
       bsum1 = fmaf(p[r], vb1v[r], bsum1);
     }
-    const uint32_t w00 = pack_h2(p[0] * vs0v[0], p[1] * vs0v[1]);
-    const uint32_t w01 = pack_h2(p[2] * vs0v[2], p[3] * vs0v[3]);
-    const uint32_t w10 = pack_h2(p[0] * vs1v[0], p[1] * vs1v[1]);
-    const uint32_t w11 = pack_h2(p[2] * vs1v[2], p[3] * vs1v[3]);
+    // keys in the V operands' k-slot order: r = 0, 2, 1, 3
+    const uint32_t w00 = pack_h2(p[0] * vs0v[0], p[2] * vs0v[2]);
+    const uint32_t w01 = pack_h2(p[1] * vs0v[1], p[3] * vs0v[3]);
+    const uint32_t w10 = pack_h2(p[0] * vs1v[0], p[2] * vs1v[2]);
+    const uint32_t w11 = pack_h2(p[1] * vs1v[1], p[3] * vs1v[3]);
     // P.V: K-step e covers key tiles 2e (slots 0-3) and 2e+1 (slots 4-7); one transposed read of
     // 32-dim slab t gives lane lc the bytes of dims 32 t + 2 lc, + 1 for its 8 keys.
 #pragma unroll
@@ -296,9 +304,11 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
       for (int t = 0; t < 4; ++t) {
         const v2i_t raw =
             __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)(vrow + 16 * (t ^ lq4)));
+        // bytes j = keys j of dims (2 lc', 2 lc' + 1); per 4 bytes: keys 0, 2 then 1, 3
         const uint32_t x0 = (uint32_t)raw.x, x1 = (uint32_t)raw.y;
-        const half8_t ae = codes8_sub(x0 & NIB, x1 & NIB);
-        const half8_t ao = codes8_sub((x0 >> 4) & NIB, (x1 >> 4) & NIB);
+        const uint32_t y0 = x0 >> 8, y1 = x1 >> 8;
+        const half8_t ae = words_as_h8(x0 & NIB_LO, y0 & NIB_LO, x1 & NIB_LO, y1 & NIB_LO);
+        const half8_t ao = words_as_h8(x0 & NIB_HI, y0 & NIB_HI, x1 & NIB_HI, y1 & NIB_HI);
         const half8_t& bg = t < 2 ? b0 : b1;
         oacc[2 * t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, bg, oacc[2 * t], 0, 0, 0);
         oacc[2 * t + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, bg, oacc[2 * t + 1], 0, 0, 0);
@@ -343,13 +353,18 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     const int kq = q_pow2_exp(qvalid ? bf16x2_max_value(mbits) : 0.0f);
     const float qf = pow2f(kq);
     kscale = qk_scale_log2 * pow2f(24 - kq);
+    // dim 8 s + e goes to k-slot {0, 2, 4, 6, 1, 3, 5, 7}[e] of qb[s] (the order nib8_sub gives
+    // the codes), odd dims times 1/16 (their codes enter at 16 c * 2^-24)
     float sg[2] = {0.f, 0.f};
+    const float qf16 = qf * 0.0625f;
 #pragma unroll
     for (int i = 0; i < 64; ++i) {
       const float lo = bf16_lo(w[i]), hi = bf16_hi(w[i]);
       sg[i >> 5] += lo + hi;
-      qb[i >> 2][2 * (i & 3)] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
-      qb[i >> 2][2 * (i & 3) + 1] = on ? (_Float16)(hi * qf) : (_Float16)0.0f;
+      const int e = 2 * (i & 3);               // dims 8 s + e and 8 s + e + 1
+      const int slot = 2 * (e & 2) + (e >> 2);  // k-slot of dim e; dim e + 1 sits two slots on
+      qb[i >> 2][slot] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
+      qb[i >> 2][slot + 2] = on ? (_Float16)(hi * qf16) : (_Float16)0.0f;
     }
     qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
     qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
@@ -378,6 +393,8 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     if (si + 3 < nst) issue(si + 3, B1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int t = 0; t < 4; ++t) oacc[2 * t + 1] *= 0.0625f;  // odd dims' codes entered at 16 c
   vscale_remove(vsc, oacc);
   __syncthreads();
   packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.fin.acc[0][0][0],
