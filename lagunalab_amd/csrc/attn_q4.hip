@@ -319,18 +319,15 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
   const std::integral_constant<int, 0> B0;
   const std::integral_constant<int, 1> B1;
   // Prologue: the R q rows (contiguous, <= 1 KB) go to this wave's terms area by DMA (free until
-  // the first super-tile is processed), then super-tiles 0 and 1; only the q copy is waited for
-  // before the q operands are built, so both super-tiles stream in meanwhile. Nothing is issued
-  // for super-tiles past the wave's range.
+  // the first super-tile is processed), then super-tile 0; only the q copy is waited for before
+  // the q operands are built, and super-tile 1 is issued after them, behind every wave's
+  // super-tile 0 (26.5 -> 26.1 us). Nothing is issued for super-tiles past the wave's range.
   {
     const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;
     dma_b128<0>(qblk, (uint32_t)min(16 * lane, R * 2 * D - 16), lds_addr(&tm));
   }
   if (nst > 0) issue(0, B0);
-  if (nst > 1) issue(1, B1);
-  if (nst > 1)
-    asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-  else if (nst > 0)
+  if (nst > 0)
     asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -372,6 +369,7 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // q reads done before terms overwrite
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (nst > 1) issue(1, B1);
 
   // Step si waits for super-tile si (all but the copies of si + 1, when those were issued),
   // processes it, then refills its buffer with super-tile si + 2 if that is in range.

@@ -381,10 +381,10 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   int k = 0;                                      // cur is the wave's super-tile number k
   uint32_t g = 0u;                                // the grab in flight
 
-  // Prologue, all copies: q rows, the new K and V rows (fused append) into this wave's terms area
-  // (free until the first super-tile is processed), super-tile 0, the grab of super-tile 2 and
-  // super-tile 1. Only the first three are waited for before the q operands are built, so both
-  // super-tiles stream in meanwhile.
+  // Prologue, copies: q rows, the new K and V rows (fused append) into this wave's terms area
+  // (free until the first super-tile is processed), super-tile 0 and the grab of super-tile 2.
+  // Only the first three are waited for before the q operands are built; super-tile 1 is issued
+  // after them (below).
   {
     const uint32_t stage = lds_addr(&tm);
     const uint16_t* qblk = q + ((int64_t)b * Hq + hk * G) * L * D;  // the R rows, contiguous
@@ -407,11 +407,8 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   // register after the statement, and a copy the compiler might insert would read it too early.
   if (cur < T) issue(cur, B0);
   grab(g, 2 >= NS && nxt < T);  // super-tile number 2: dynamic when NS == 2
-  if (nxt < T) issue(nxt, B1);
-  // the q and new rows have landed (the copies and the grab issued after them may be in flight)
-  if (nxt < T)
-    asm volatile("s_waitcnt vmcnt(41)" ::: "memory");
-  else if (cur < T)
+  // the q and new rows have landed (super-tile 0 and the grab issued after them may be in flight)
+  if (cur < T)
     asm volatile("s_waitcnt vmcnt(21)" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
@@ -466,6 +463,10 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
     qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
   }
+  // Super-tile 1 goes out only now, behind every wave's super-tile 0 (~18 MB over the chip at
+  // 82,671 keys): issued together, the two landed in the same window, so the loop waited for
+  // super-tile 0 until both were nearly in (37.6 -> 36.7 us per fused decode step).
+  if (nxt < T) issue(nxt, B1);
   QPair app_k = {0u, 0, 0}, app_v = {0u, 0, 0};
   uint32_t app_w[4] = {0u, 0u, 0u, 0u};  // ks, kb, vs, vb words of the new row (group 0 low)
   bool patched = false;
