@@ -1,16 +1,18 @@
 // Quantize-on-append and dequantize for the affine group-quantized KV cache.
 //
 // lq_quantize_append replaces mx.quantize as called by mlx-lm QuantizedKVCache.update_and_fetch
-// from DequantKVCache.update_and_fetch (laguna_mlx/cache.py:89-90). A lane takes 8 consecutive
-// values of a row (one 16-byte load) and the gs / 8 lanes of a group (32, 64 or 128 values, side
-// by side in one wave) reduce its min and max with DPP; every lane then derives the group's
-// scale/bias with IEEE fp32 arithmetic (correctly rounded division, round-half-away) and writes
-// its 8 codes (8 or 4 bytes), and the group's first lane writes the bf16 scale and bias. The
+// from DequantKVCache.update_and_fetch (laguna_mlx/cache.py:89-90). One lane quantizes one whole
+// group (32, 64 or 128 values): a wave's 64 groups are contiguous in the source, so they go to LDS
+// with plain coalesced DMA copies (each copy fills 1 KB; a group's 16-byte chunks land at swizzled
+// positions, chunk c of group g at c ^ s(g)), and each lane reads its own group back with
+// conflict-free 16-byte LDS reads. The lane then takes the group's min and max in registers (no
+// cross-lane reduction), derives scale and bias once with IEEE fp32 arithmetic (correctly rounded
+// division, round-half-away), and writes the group's codes and its bf16 scale and bias. The
 // arithmetic is bit-for-bit the MLX affine quantizer restated in oracle/quantize.py.
 //
 // lq_dequantize replaces mx.dequantize on the unfused path (cache.py:99-100):
 // bf16(fp32(scale) * code + fp32(bias)) with an unfused multiply then add.
-#include "common.h"
+#include "attn_dev.h"
 
 namespace lq {
 namespace {
@@ -34,109 +36,137 @@ __device__ __forceinline__ uint32_t fdiv_u(uint32_t n, FastDiv f) {
 // affine_code. Fast path: u = (x - bias) * (1 / scale) + 0.5 (v_rcp_f32, 1 ulp) is within
 // 6.1e-5 of fl(fl(x - bias) / scale) + 0.5 for quotients below 512 (ours stay below 257), so
 // floor(u) is the code unless u lies within 2e-4 of an integer; those lanes (and NaN/inf) take the
-// correctly rounded division instead. Returns the code; sets `slow` for the lanes that need it.
+// correctly rounded division instead. u >= 0 up to rounding (the bias is the group's edge on the
+// side the scale's sign points away from), so truncation is the floor and a slightly negative u
+// converts to 0, as its floor clamps there. Returns the code; sets `slow` for the lanes that need
+// the division.
 template <int BITS>
 __device__ __forceinline__ uint32_t fast_code(float x, const AffineParams& p, float rs, bool& slow) {
-  constexpr float n_bins = (float)((1 << BITS) - 1);
   const float u = fmaf(x - p.bias, rs, 0.5f);
-  const float f = u - floorf(u);
+  const float f = __builtin_amdgcn_fractf(u);
   slow = !(fabsf(f - 0.5f) < 0.4998f);
-  return (uint32_t)fminf(floorf(u), n_bins);
+  return min((uint32_t)u, (uint32_t)((1 << BITS) - 1));
 }
 
-// LPG = group_size / 8 lanes per group; UN chunks of 8 values per lane per pass (loads issued
-// together). Chunks [0, chunks) go to target a, [chunks, 2 chunks) to target b when `two` (K and V
-// of one update in one launch). Chunk c of a target: row c / cpr (row = bh L + l, cache row
-// bh cap + offset + l), values 8 (c % cpr) .. + 7.
-template <int BITS, int LPG, int UN>
-__global__ __launch_bounds__(256) void quantize_append_kernel(
-    AppendTarget a, AppendTarget b, int64_t chunks, int64_t total, FastDiv fd_cpr, FastDiv fd_L,
-    int cpr, int L, int64_t cap, int64_t offset) {
+// One lane per group of GS values (CH = GS / 8 chunks of 16 bytes); a wave takes 64 consecutive
+// groups (every group of the update lies in one row: GS divides the head dim). Groups [0, groups_a)
+// belong to target a, [groups_a, groups) to target b (K and V of one update in one launch). Group
+// q of a target: row q / gpr (row = bh L + l, cache row bh cap + offset + l), group q % gpr of it,
+// source values GS q .. GS q + GS - 1.
+//
+// LDS layout per wave: group g's CH chunks at 16-byte slots CH g + (c ^ s(g)), s(g) = (g / (16 /
+// CH)) % CH, so that the 16 lanes of one ds_read_b128 pass hit 16 different bank groups. Copy i of
+// lane l fills slot 64 i + l.
+template <int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_group_kernel(
+    AppendTarget a, AppendTarget b, int64_t groups_a, int64_t groups, FastDiv fd_gpr, FastDiv fd_L,
+    int gpr, int L, int64_t cap, int64_t offset) {
+  constexpr int CH = GS / 8;
+  constexpr int CB = 2 * GS;          // source bytes per group
+  constexpr int CPB = BITS * GS / 8;  // code bytes per group
+  __shared__ __attribute__((aligned(16))) uint8_t stage[4][64 * CB];
   const int lane = threadIdx.x & 63;
-  const int gpr = cpr / LPG;  // groups per row
-  const int64_t stride = (int64_t)gridDim.x * 256 * UN;
-  for (int64_t base = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 * UN; base < total;
-       base += stride) {  // wave-uniform
-    uint4 raw[UN];
-    int64_t cc[UN];
-    bool sec[UN], in[UN];
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
+  const uint32_t st_lds = attn::lds_addr(&stage[wv][0]);
+  auto swz = [](int g) { return (g / (16 / CH)) % CH; };
+  // per-lane byte offset of copy i within the wave's 64 CB source bytes (same for every wave)
+  uint32_t voff[CH];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int64_t i = base + 64 * u + lane;
-      in[u] = i < total;
-      sec[u] = i >= chunks;
-      cc[u] = sec[u] ? i - chunks : i;
-      const uint16_t* src = sec[u] ? b.src : a.src;
-      raw[u] = in[u] ? *reinterpret_cast<const uint4*>(src + cc[u] * 8) : make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < CH; ++i) {
+    const int slot = 64 * i + lane, g = slot / CH, pos = slot % CH;
+    voff[i] = (uint32_t)(g * CB + 16 * (pos ^ swz(g)));
+  }
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t wbase = ((int64_t)blockIdx.x * 4 + wv) * 64; wbase < groups; wbase += stride) {
+    // copies: one target and no tail (the common case) with a scalar base, else per-lane addresses
+    if (wbase + 64 <= groups && (wbase + 64 <= groups_a || wbase >= groups_a)) {
+      const bool in_a = wbase < groups_a;
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(in_a ? a.src : b.src) +
+                            (in_a ? wbase : wbase - groups_a) * CB;
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                     :: "v"(voff[i]), "s"(base), "s"(st_lds + 1024u * i) : "memory");
+    } else {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int slot = 64 * i + lane;
+        const int64_t g = min(wbase + slot / CH, groups - 1);  // past the end: a valid group
+        const bool in_a = g < groups_a;
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(in_a ? a.src : b.src) +
+                             (in_a ? g : g - groups_a) * CB + (voff[i] % CB);
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                     :: "v"(src), "s"(st_lds + 1024u * i) : "memory");
+      }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // this lane's group, in registers
+    float x[GS];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-      float x[8];
+    for (int c = 0; c < CH; ++c) {
+      const uint4 u = *reinterpret_cast<const uint4*>(&stage[wv][16 * (CH * lane + (c ^ swz(lane)))]);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        x[2 * j] = bf16_lo(w[j]);
-        x[2 * j + 1] = bf16_hi(w[j]);
+        x[8 * c + 2 * j] = bf16_lo(w[j]);
+        x[8 * c + 2 * j + 1] = bf16_hi(w[j]);
       }
-      float lo = INFINITY, hi = -INFINITY;
-      if (in[u]) {
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the next copies
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // min and max with v_min3/v_max3 as written: fminf/fmaxf would first quiet every decoded
+    // value (a possible signalling NaN) with one more instruction each
+    float lo = x[0], hi = x[0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          lo = fminf(lo, x[j]);
-          hi = fmaxf(hi, x[j]);
+    for (int k = 1; k + 1 < GS; k += 2) {
+      asm("v_min3_f32 %0, %1, %2, %3" : "=v"(lo) : "v"(lo), "v"(x[k]), "v"(x[k + 1]));
+      asm("v_max3_f32 %0, %1, %2, %3" : "=v"(hi) : "v"(hi), "v"(x[k]), "v"(x[k + 1]));
+    }
+    asm("v_min_f32 %0, %1, %2" : "=v"(lo) : "v"(lo), "v"(x[GS - 1]));
+    asm("v_max_f32 %0, %1, %2" : "=v"(hi) : "v"(hi), "v"(x[GS - 1]));
+    const AffineParams p = affine_params<BITS>(lo, hi);
+    const float rs = __builtin_amdgcn_rcpf(p.scale);
+    // codes, one output dword (4 or 8 codes) at a time; the rare slow lanes redo their values
+    constexpr int PER = 32 / BITS;  // codes per dword
+    uint32_t out[GS / PER];
+#pragma unroll
+    for (int d = 0; d < GS / PER; ++d) {
+      uint32_t c[PER];
+      bool any = false;
+#pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        bool sl;
+        c[r] = fast_code<BITS>(x[PER * d + r], p, rs, sl);
+        any |= sl;
+      }
+      if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+          bool sl;
+          (void)fast_code<BITS>(x[PER * d + r], p, rs, sl);
+          if (sl) c[r] = affine_code<BITS>(x[PER * d + r], p);
         }
       }
-      // group min / max over its LPG lanes (quads, then half rows, then rows)
-      lo = fminf(lo, dpp<DPP_QUAD_XOR1>(lo));
-      hi = fmaxf(hi, dpp<DPP_QUAD_XOR1>(hi));
-      lo = fminf(lo, dpp<DPP_QUAD_XOR2>(lo));
-      hi = fmaxf(hi, dpp<DPP_QUAD_XOR2>(hi));
-      if (LPG >= 8) {
-        lo = fminf(lo, dpp<DPP_ROW_HALF_MIRROR>(lo));
-        hi = fmaxf(hi, dpp<DPP_ROW_HALF_MIRROR>(hi));
-      }
-      if (LPG >= 16) {
-        lo = fminf(lo, dpp<DPP_ROW_MIRROR>(lo));
-        hi = fmaxf(hi, dpp<DPP_ROW_MIRROR>(hi));
-      }
-      const AffineParams p = affine_params<BITS>(lo, hi);
-      const float rs = __builtin_amdgcn_rcpf(p.scale);
-      uint32_t c[8];
-      bool any_slow = false, slow[8];
+      uint32_t wd = c[0];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        c[j] = fast_code<BITS>(x[j], p, rs, slow[j]);
-        any_slow |= slow[j];
-      }
-      if (__builtin_amdgcn_ballot_w64(any_slow && in[u])) {  // rare: a value near a rounding edge
+      for (int r = 1; r < PER; ++r) wd |= c[r] << (BITS * r);
+      out[d] = wd;
+    }
+    const int64_t gi = wbase + lane;
+    if (gi < groups) {
+      const bool in_a = gi < groups_a;
+      const uint32_t q = (uint32_t)(in_a ? gi : gi - groups_a);
+      const uint32_t row = fdiv_u(q, fd_gpr);
+      const int gq = (int)(q - row * (uint32_t)gpr);
+      const uint32_t bh = fdiv_u(row, fd_L);
+      const int64_t drow = (int64_t)bh * cap + offset + (int64_t)(row - bh * (uint32_t)L);
+      uint8_t* codes = (in_a ? a.codes : b.codes) + drow * ((int64_t)gpr * CPB) + (int64_t)gq * CPB;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (slow[j]) c[j] = affine_code<BITS>(x[j], p);
-      }
-      if (in[u]) {
-        const uint32_t cu = (uint32_t)cc[u];
-        const uint32_t row = fdiv_u(cu, fd_cpr);
-        const int ch = (int)(cu - row * (uint32_t)cpr);
-        const uint32_t bh = fdiv_u(row, fd_L);
-        const int64_t drow = (int64_t)bh * cap + offset + (int64_t)(row - bh * (uint32_t)L);
-        uint8_t* codes = sec[u] ? b.codes : a.codes;
-        if (BITS == 8) {
-          const uint32_t d0 = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-          const uint32_t d1 = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-          *reinterpret_cast<uint2*>(codes + drow * (8 * cpr) + 8 * ch) = make_uint2(d0, d1);
-        } else {  // element 2j in the low nibble of byte j
-          uint32_t d0 = 0u;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) d0 |= c[j] << (4 * j);
-          *reinterpret_cast<uint32_t*>(codes + drow * (4 * cpr) + 4 * ch) = d0;
-        }
-        if (ch % LPG == 0) {
-          uint16_t* scales = sec[u] ? b.scales : a.scales;
-          uint16_t* biases = sec[u] ? b.biases : a.biases;
-          scales[drow * gpr + ch / LPG] = f32_to_bf16(p.scale);
-          biases[drow * gpr + ch / LPG] = f32_to_bf16(p.bias);
-        }
-      }
+      for (int d = 0; d < GS / PER; d += 4)
+        *reinterpret_cast<uint4*>(codes + 4 * d) = make_uint4(out[d], out[d + 1], out[d + 2], out[d + 3]);
+      (in_a ? a.scales : b.scales)[drow * gpr + gq] = f32_to_bf16(p.scale);
+      (in_a ? a.biases : b.biases)[drow * gpr + gq] = f32_to_bf16(p.bias);
     }
   }
 }
@@ -184,14 +214,12 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
   }
 }
 
-template <int BITS, int LPG>
-void launch_quantize(AppendTarget a, AppendTarget b, int64_t chunks, int64_t total, int cpr, int L,
-                     int64_t cap, int64_t offset, hipStream_t st) {
-  constexpr int UN = 4;
-  const int64_t waves = (total + 64 * UN - 1) / (64 * UN);
-  const int64_t blocks = std::min<int64_t>((waves + 3) / 4, 8192);
-  quantize_append_kernel<BITS, LPG, UN><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-      a, b, chunks, total, make_fastdiv((uint32_t)cpr), make_fastdiv((uint32_t)L), cpr, L, cap,
+template <int BITS, int GS>
+void launch_quantize(AppendTarget a, AppendTarget b, int64_t groups_a, int64_t groups, int gpr,
+                     int L, int64_t cap, int64_t offset, hipStream_t st) {
+  const int64_t blocks = std::min<int64_t>((groups + 255) / 256, 1 << 20);
+  quantize_group_kernel<BITS, GS><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+      a, b, groups_a, groups, make_fastdiv((uint32_t)gpr), make_fastdiv((uint32_t)L), gpr, L, cap,
       offset);
 }
 
@@ -212,22 +240,23 @@ int quantize_append(AppendTarget a, AppendTarget b, int two, int64_t B, int64_t 
   LQ_CHECK_ARG(a.src && a.codes && a.scales && a.biases, "null pointer");
   LQ_CHECK_ARG(!two || (b.src && b.codes && b.scales && b.biases), "null pointer");
   if (L == 0) return LQ_OK;
-  const int64_t chunks = B * H * L * (D / 8);  // 8 values each
-  const int64_t total = (two ? 2 : 1) * chunks;
-  LQ_CHECK_ARG(total < (int64_t)1 << 31 && L < (int64_t)1 << 31 && D / 8 < (int64_t)1 << 31,
-               "append of %lld values is too large for one call", (long long)(total * 8));
-  const int cpr = (int)(D / 8);
+  const int64_t groups_a = B * H * L * (D / group_size);
+  const int64_t groups = (two ? 2 : 1) * groups_a;
+  LQ_CHECK_ARG(groups < (int64_t)1 << 31 && L < (int64_t)1 << 31,
+               "append of %lld values is too large for one call",
+               (long long)(groups * group_size));
+  const int gpr = (int)(D / group_size);
   if (group_size == 32) {
-    if (bits == 8) launch_quantize<8, 4>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
-    else launch_quantize<4, 4>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    if (bits == 8) launch_quantize<8, 32>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 32>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
   } else if (group_size == 64) {
-    if (bits == 8) launch_quantize<8, 8>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
-    else launch_quantize<4, 8>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    if (bits == 8) launch_quantize<8, 64>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 64>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
   } else {
-    if (bits == 8) launch_quantize<8, 16>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
-    else launch_quantize<4, 16>(a, b, chunks, total, cpr, (int)L, cap, offset, st);
+    if (bits == 8) launch_quantize<8, 128>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
+    else launch_quantize<4, 128>(a, b, groups_a, groups, gpr, (int)L, cap, offset, st);
   }
-  LQ_CHECK_LAUNCH("quantize_append_kernel");
+  LQ_CHECK_LAUNCH("quantize_group_kernel");
   return LQ_OK;
 }
 
