@@ -32,7 +32,7 @@
 //    owner patches the staged rows into its LDS copy of the super-tile after the copies land (the
 //    copies may have read the rows before or while they were stored), once an LDS count says the
 //    staging waves are done. No other wave uses those rows. Same arithmetic as
-//    quantize_append_kernel, so the codes agree.
+//    quantize_group_kernel, so the codes agree.
 //  * Partials (m, l, acc) per (workgroup, query row) go to the workspace; decode_merge_kernel
 //    merges them (at 16+ rows per KV head the partials of 32 workgroups are ~330 KB per head, too
 //    much for one workgroup to merge at the end of the attention kernel).

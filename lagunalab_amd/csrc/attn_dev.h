@@ -196,7 +196,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // One 128-element bf16 row quantized to 8 bits in groups of 64 by one wave, lane l holding
 // elements 2l and 2l+1 (group l / 32): the two codes of the lane (low 16 bits) and the bf16 scale
-// and bias of its group. Same arithmetic as quantize_append_kernel (affine_params/affine_code on
+// and bias of its group. Same arithmetic as quantize_group_kernel (affine_params/affine_code on
 // the group min and max), so the codes agree bit for bit. All 64 lanes must be active.
 struct QPair {
   uint32_t codes;
