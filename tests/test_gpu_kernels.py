@@ -751,7 +751,9 @@ def test_fused_verify_step_in_cache(dev):
 @pytest.mark.parametrize("n,L,G,Hkv,B", [(3000, 100, 4, 2, 1), (700, 64, 8, 2, 1), (33, 33, 1, 4, 1),
                                          (5000, 300, 4, 8, 1), (1200, 260, 2, 2, 2),
                                          (513, 513, 4, 1, 1), (4200, 17, 8, 8, 1),
-                                         (2000, 17, 16, 1, 1), (900, 40, 3, 2, 1)])
+                                         (2000, 17, 16, 1, 1), (900, 40, 3, 2, 1),
+                                         (1536, 1536, 4, 2, 1), (1000, 1000, 8, 1, 1),
+                                         (900, 900, 2, 2, 2), (2500, 1500, 4, 2, 1)])
 def test_prefill_matches_causal_oracle(dev, n, L, G, Hkv, B):
     """q8_prefill_attention over n rows whose last L are the chunk's own: against the causal
     fused-arithmetic and unfused oracles. G in {1, 2, 4, 8}: the prefill kernel (blocks of
