@@ -178,6 +178,27 @@ def test_decode_matches_unfused_oracle(dev, n, G, B):
     assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale), f"unfused n={n} G={G}", at, rt)
 
 
+@pytest.mark.parametrize("n", [65536, 65537])
+def test_decode_at_the_dense_packed_boundary(dev, n):
+    """One sequence, 32q/8kv: up to 65,536 rows decode runs the dense kernel and a merge launch,
+    past it the packed kernel with its merge inside. Both sides of the boundary against the
+    oracle, plain and fused (append row n - 1 inside the step)."""
+    from lagunalab_amd.q8_attn import decode_append_attention, q8_decode_attention
+    rng = np.random.default_rng(n)
+    Hkv, G, B = 8, 4, 1
+    cap = (n + 256) // 256 * 256
+    kq, vq = make_cache(rng, B, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (B, Hkv * G, 1, 128))
+    got = q8_decode_attention(to_dev_bf16(q, dev), kq, vq, n, 0.09)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"decode n={n}")
+    k1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    v1 = to_dev_bf16(Q.randn_bf16(rng, (B, Hkv, 1, 128)), dev)
+    got = decode_append_attention(to_dev_bf16(q, dev), k1, v1, kq, vq, n=n - 1, scale=0.09)
+    kn, vn = cache_np(kq), cache_np(vq)
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, 0.09), f"fused step n={n}")
+
+
 @pytest.mark.parametrize("n", [8500, 11000, 13500])
 def test_decode_two_static_super_tiles(dev, n):
     """The packed kernel (two sequences, so that short lengths take it too), 8 KV heads: each
