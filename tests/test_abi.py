@@ -147,3 +147,25 @@ def test_decode_split_plan_fills_one_wave(lib):
     assert splits([1000]) == 4        # at least 256 keys per split
     assert splits([1, 1, 1]) == 3     # one split per sequence at least
     assert splits([5000] * 40) == 40  # more sequences than the budget: one split each
+
+
+def test_decode_kernel_choice_at_the_length_boundary(lib):
+    """One sequence of up to 65,536 rows (G L <= 4) takes the dense kernel and a merge launch:
+    its workspace holds the normalized q / k rows behind the partials; from 65,537 rows, or with
+    two sequences, the packed kernel merges inside and needs only counters + partials."""
+    import ctypes as C
+
+    def ws(lens, Hq=32, Hkv=8, kind=8):
+        arr = (C.c_int32 * len(lens))(*lens)
+        return lib.lq_decode_workspace_bytes(kind, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
+    per = 8 * 4 * (128 * 4 + 8)  # partial bytes per split, 32q/8kv
+    packed = ws([65537])
+    assert (packed - _lib.LQ_WS_ZERO_BYTES) % per == 0 and (packed - _lib.LQ_WS_ZERO_BYTES) // per == 32
+    dense = ws([65536])
+    partials = _lib.LQ_WS_ZERO_BYTES + 32 * per
+    assert dense == (partials + 255) // 256 * 256 + (32 + 8) * 128 * 2
+    two = ws([65536, 65536])
+    assert (two - _lib.LQ_WS_ZERO_BYTES) % per == 0  # a batch: packed, no norm rows
+    # the 4-bit and bf16 kinds always run their packed kernels
+    assert (ws([4096], kind=4) - _lib.LQ_WS_ZERO_BYTES) % per == 0
+    assert (ws([4096], kind=16) - _lib.LQ_WS_ZERO_BYTES) % per == 0
