@@ -155,6 +155,8 @@ def test_decode_kernel_choice_at_the_length_boundary(lib):
     two sequences, the packed kernel merges inside and needs only counters + partials."""
     import ctypes as C
 
+    from lagunalab_amd import _lib
+
     def ws(lens, Hq=32, Hkv=8, kind=8):
         arr = (C.c_int32 * len(lens))(*lens)
         return lib.lq_decode_workspace_bytes(kind, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
