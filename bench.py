@@ -46,6 +46,10 @@ def parse():
     p.add_argument("--roofline-calls", type=int, default=128,
                    help="plain attention calls timed in groups of 8 after the timed steps "
                         "(attn_us_per_call; the roofline with --separate-append)")
+    p.add_argument("--settle-ms", type=float, default=500.0,
+                   help="before the warm-up, run back-to-back attention calls over the rotating "
+                        "caches for this long (GPU time, outside the timed region) so that a run "
+                        "on a just-acquired GPU is timed at its settled clocks; 0 disables it")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline sample: calls are repeated until this much time has passed")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -210,6 +214,28 @@ def _gpu_groups(stream, calls, group, fn):
         pairs.append(e)
     torch.cuda.synchronize()
     return [a.elapsed_time(b) / group for a, b in pairs]
+
+
+def settle(stream, ms, fn, group=256):
+    """Runs fn(j) back to back in groups of `group` launches until their GPU time (events on the
+    launch stream) adds up to `ms`. A GPU that has just been acquired runs its first milliseconds
+    of work below its settled clocks; this phase sits before the warm-up, outside the timed
+    region. Returns what it did, for the JSON line."""
+    import torch
+    if ms <= 0:
+        return {"ms": 0.0, "calls": 0}
+    done, calls, t0 = 0.0, 0, time.perf_counter()
+    while done < ms:
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record(stream)
+        for k in range(group):
+            fn(calls + k)
+        e[1].record(stream)
+        e[1].synchronize()
+        done += e[0].elapsed_time(e[1])
+        calls += group
+    return {"ms": round(done, 1), "calls": calls,
+            "wall_ms": round((time.perf_counter() - t0) * 1e3, 1)}
 
 
 def _result(metric, value, unit, hib, ms, args, dtype, config, extra):
@@ -791,57 +817,64 @@ def main():
     offsets = [ctx] * nl
     torch.cuda.synchronize()
 
-    def append(i, lay, off):
+    def attend_args(i, lay, n):
         (kc, ks, kb), (vc, vs, vb) = lay
-        return lib.lq_quantize_append_kv(ks_new[i].data_ptr(), vs_new[i].data_ptr(), 1, HKV, 1, D,
-                                         kc.data_ptr(), ks.data_ptr(), kb.data_ptr(),
-                                         vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), cap, off,
-                                         8, GS, sp)
+        return (8, qs[i].data_ptr(), kc.data_ptr(), ks.data_ptr(), kb.data_ptr(), vc.data_ptr(),
+                vs.data_ptr(), vb.data_ptr(), 1, HQ, HKV, D, cap, n, None, D ** -0.5,
+                out.data_ptr(), ws.data_ptr(), ws.numel(), sp)
 
     def attend(i, lay, n):
-        (kc, ks, kb), (vc, vs, vb) = lay
-        return lib.lq_decode_attn(8, qs[i].data_ptr(), kc.data_ptr(), ks.data_ptr(),
-                                  kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1,
-                                  HQ, HKV, D, cap, n, None, D ** -0.5, out.data_ptr(),
-                                  ws.data_ptr(), ws.numel(), sp)
+        return lib.lq_decode_attn(*attend_args(i, lay, n))
 
-    def fused_step(i, lay, off):
+    def step_launches(i):
+        """Step i as the (entry point, arguments) of its launches: the fused step appends at row
+        ctx + i of layer i % nl and attends over ctx + i + 1 rows. Built before any timing, so
+        that the timed loop only issues the calls."""
+        lay = layers[i % nl]
         (kc, ks, kb), (vc, vs, vb) = lay
-        return lib.lq_q8_decode_append_attn(qs[i].data_ptr(), ks_new[i].data_ptr(),
-                                            vs_new[i].data_ptr(), kc.data_ptr(), ks.data_ptr(),
-                                            kb.data_ptr(), vc.data_ptr(), vs.data_ptr(),
-                                            vb.data_ptr(), 1, HQ, HKV, D, cap, off, None,
-                                            D ** -0.5, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                            sp)
-
-    def step(i):
-        li = i % nl
         off = ctx + i
         if args.separate_append:
-            st = append(i, layers[li], off)
-            st |= attend(i, layers[li], off + 1)
-        else:
-            st = fused_step(i, layers[li], off)
-        offsets[li] = off + 1
-        if st:
-            _lib.check(st, "bench step")
-        return off + 1
+            return [(lib.lq_quantize_append_kv,
+                     (ks_new[i].data_ptr(), vs_new[i].data_ptr(), 1, HKV, 1, D, kc.data_ptr(),
+                      ks.data_ptr(), kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(),
+                      cap, off, 8, GS, sp)),
+                    (lib.lq_decode_attn, attend_args(i, lay, off + 1))]
+        return [(lib.lq_q8_decode_append_attn,
+                 (qs[i].data_ptr(), ks_new[i].data_ptr(), vs_new[i].data_ptr(), kc.data_ptr(),
+                  ks.data_ptr(), kb.data_ptr(), vc.data_ptr(), vs.data_ptr(), vb.data_ptr(), 1, HQ,
+                  HKV, D, cap, off, None, D ** -0.5, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                  sp))]
 
-    for i in range(args.warmup):
-        step(i)
+    launches = [step_launches(i) for i in range(total_steps)]
+
+    def run_steps(first, count):
+        """Issues steps first .. first + count - 1; returns the OR of their status codes."""
+        st = 0
+        for i in range(first, first + count):
+            for fn, a in launches[i]:
+                st |= fn(*a)
+        return st
+
+    # ---- settle: plain attention calls (the same kernel without the append, n = ctx rows, which
+    # every cache holds) over the rotating caches, then the warm-up steps
+    settled = settle(stream, args.settle_ms,
+                     lambda j: _lib.check(attend(j % total_steps, layers[j % nl], ctx), "settle"))
+    _lib.check(run_steps(0, args.warmup), "warm-up step")
     torch.cuda.synchronize()
 
     # ---- timed region: K steps, bracketed by one pair of events on the launch stream
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
-    ns = []
     torch.cuda.synchronize()
     t_start.record(stream)
-    for j in range(args.steps):
-        ns.append(step(args.warmup + j))
+    st = run_steps(args.warmup, args.steps)
     t_end.record(stream)
     torch.cuda.synchronize()
+    _lib.check(st, "timed step")
     total_ms = t_start.elapsed_time(t_end)
+    ns = [ctx + i + 1 for i in range(args.warmup, total_steps)]  # rows attended per timed step
+    for i in range(total_steps):
+        offsets[i % nl] = ctx + i + 1
 
     # ---- roofline of the dominant kernel. Fused steps: each timed step is exactly one launch of
     # lq_q8_decode_append_attn, so its average launch duration is the timed region's time / K
@@ -885,11 +918,17 @@ def main():
         k_ms, k_bytes, k_calls = total_ms / args.steps, sum(step_bytes) / len(step_bytes), args.steps
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
 
-    traffic = None
+    # HBM bytes per fused step: not measured in this run (hardware counters need a profiler run
+    # of their own); read from the committed record of two rocprofv3 --pmc passes (FETCH_SIZE,
+    # then WRITE_SIZE) of this same workload, scaled by a plain-copy calibration, and labelled so.
+    traffic, traffic_src = None, None
     tf = ROOT / "profiles" / "q8_decode_traffic.json"
     if tf.exists() and HQ == 32 and not args.separate_append and ctx == 82671:
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_call")
+            traffic_src = ("copied from profiles/q8_decode_traffic.json (rocprofv3 --pmc FETCH_SIZE "
+                           "and WRITE_SIZE passes of this workload, scaled by a plain-copy "
+                           "calibration), not measured in this run")
         except Exception:
             traffic = None
 
@@ -911,9 +950,10 @@ def main():
         "attn_us_per_call": ({"mean": round(attn_avg_ms * 1e3, 2), "median": round(attn_med_ms * 1e3, 2)}
                              if attn_ms else None),
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 2),
+        "settle": settled,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": kernel, "us_per_launch": round(k_ms * 1e3, 2),
+                     "traffic_source": traffic_src, "kernel": kernel, "us_per_launch": round(k_ms * 1e3, 2),
                      "launches_timed": k_calls, "bytes_per_call": int(k_bytes)},
         "vs_baseline_ref": "reference fused q8 kernel on an M4 GPU: 12.24 ms/call = 14.69 GB/s",
     }

@@ -81,6 +81,8 @@ int lq_dequantize(const uint8_t* codes, const uint16_t* scales, const uint16_t* 
 /*
  * Scratch bytes for lq_decode_attn with the same B / Hq / Hkv / lengths. `lens_host` (host, B
  * entries) may be NULL, then every sequence has length n. Returns a negative value on bad args.
+ * The size never falls as a length grows (same kind, B, Hq, Hkv): a workspace sized for a
+ * session's longest lengths serves every shorter call of the same shape.
  */
 int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                   int64_t n, const int32_t* lens_host);
@@ -127,7 +129,7 @@ int lq_q8_decode_append_attn(const uint16_t* q, const uint16_t* k_new, const uin
                              void* stream);
 
 /*
- * Scratch bytes for lq_q8_verify_attn.
+ * Scratch bytes for lq_q8_verify_attn; like lq_decode_workspace_bytes, never falling as n grows.
  */
 int64_t lq_verify_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                                   int64_t n);
@@ -309,8 +311,10 @@ int lq_gemv_norm_rope(const uint16_t* W, const uint16_t* x, const uint16_t* norm
  * 4 MiB device array, one per GPU the library runs on, held until the process ends; a call that
  * would need more (lq_decode_workspace_bytes of its shape) returns LQ_EWORKSPACE before any launch
  * (32q/8kv at any length needs about 0.66 MiB). The first call on a device queues a clear of the
- * array's counters on its stream; every call leaves them clear. All calls on one GPU share the
- * array: calls that overlap on one GPU (concurrent streams) race.
+ * array's counters on its stream (it may be made during a graph capture); every call leaves them
+ * clear. All calls on one GPU share the array and the first call binds it to its stream: a later
+ * call on another stream returns LQ_EINVAL before any launch. Replays of a captured graph that
+ * overlap each other or an eager call on another stream still race (the library cannot see them).
  */
 int lq_q8_decode_append_attn_noalloc(const uint16_t* q, const uint16_t* k_new,
                                      const uint16_t* v_new, uint8_t* kc, uint16_t* ks,

@@ -1,4 +1,6 @@
 // Library-wide C ABI pieces: version, thread-local error text, device properties.
+#include <atomic>
+
 #include "common.h"
 
 namespace lq {
@@ -19,17 +21,19 @@ void set_error(const char* fmt, ...) {
 void clear_error() { g_error.clear(); }
 
 int device_cu_count() {
-  static int cached[64] = {0};
+  // one slot per device, filled by whichever host thread asks first (every thread computes the
+  // same value, so a relaxed atomic store and load are enough)
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus < 1)
       cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 }  // namespace lq

@@ -143,11 +143,14 @@ int64_t make_plan(int64_t B, int64_t Hkv, int64_t n, const int32_t* lens, int64_
   return s;
 }
 
-// Resident workgroups per CU for an attention kernel (cached per kernel).
+// Resident workgroups per CU for an attention kernel (cached per kernel; host threads may plan
+// calls concurrently, so the cache is read and filled under a lock).
 int attn_occupancy(QAttnFn fn, int threads) {
+  static std::mutex mu;
   static QAttnFn fns[32];
   static int occ[32];
   static int nf = 0;
+  std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < nf; ++i)
     if (fns[i] == fn) return occ[i];
   int k = 0;
@@ -232,6 +235,31 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   return S;
 }
 
+int64_t attn_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n,
+                             const int32_t* lens) {
+  DecodePlan plan;
+  AttnKernel k;
+  int64_t ws = 0;
+  if (attn_plan(kind, B, Hq, Hkv, L, n, lens, 0, plan, k, ws) < 0) return -1;
+  const int64_t longest = lens ? lens[0] : n;
+  const int64_t R = (Hq / Hkv) * L;
+  if (kind != LQ_KV_Q8) {
+    // Chunked plans (4-bit, bf16): the chunk is rounded up, so the split count can fall by one
+    // as a length grows; report the plan's bound instead (its chunk covers the keys of all
+    // sequences in at most per_head splits, plus one partial split per sequence, and at most
+    // MAX_SPLITS per sequence).
+    const int64_t per_head =
+        std::max<int64_t>(1, attn_occupancy(k.fn, k.threads) * device_cu_count() / Hkv);
+    const int64_t smax = std::min<int64_t>(per_head + B, MAX_SPLITS * B);
+    ws = std::max(ws, WS_COUNTER_BYTES + smax * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2)));
+  } else if (B == 1 && longest > DENSE_BELOW && R <= 4) {
+    int64_t dense = 0;
+    if (attn_plan(kind, 1, Hq, Hkv, L, DENSE_BELOW, nullptr, 0, plan, k, dense) < 0) return -1;
+    ws = std::max(ws, dense);
+  }
+  return ws;
+}
+
 }  // namespace lq
 
 extern "C" int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv,
@@ -246,13 +274,8 @@ extern "C" int64_t lq_decode_workspace_bytes(int kind, int64_t B, int64_t Hq, in
     set_error("kv kind %d not supported for these shapes (4-bit and bf16: Hq / Hkv <= 4)", kind);
     return -1;
   }
-  DecodePlan plan;
-  AttnKernel k;
-  int64_t ws = 0;
-  if (attn_plan(kind, B, Hq, Hkv, 1, n, lens_host, 0, plan, k, ws) < 0) {
-    set_error("bad sequence lengths");
-    return -1;
-  }
+  const int64_t ws = attn_workspace_bytes(kind, B, Hq, Hkv, 1, n, lens_host);
+  if (ws < 0) set_error("bad sequence lengths");
   return ws;
 }
 
@@ -454,6 +477,10 @@ constexpr int MAX_DEVICES = 64;
 std::mutex scratch_mu;
 void* scratch_ptr[MAX_DEVICES];  // this device's copy of `scratch`, from hipGetSymbolAddress
 bool scratch_cleared[MAX_DEVICES];
+// The stream of the first call on each device: every later call must be on it, so that calls
+// sharing the device's scratch are ordered (calls on two streams could overlap and race on it).
+hipStream_t scratch_stream[MAX_DEVICES];
+bool scratch_bound[MAX_DEVICES];
 
 __global__ void clear_words_kernel(uint32_t* p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
@@ -469,12 +496,18 @@ int clear_scratch_counters(void* p, hipStream_t st) {
 }
 
 // The current device's scratch address (looked up once per device with that device current,
-// kept for later calls); on its first use the counter area is cleared on `st`.
+// kept for later calls); on its first use the counter area is cleared on `st`. A call on another
+// stream than the device's first call is refused before anything is launched.
 int current_scratch(hipStream_t st, void** out) {
   int dev = 0;
   LQ_CHECK_HIP(hipGetDevice(&dev));
   LQ_CHECK_ARG(dev >= 0 && dev < MAX_DEVICES, "device %d outside [0, %d)", dev, MAX_DEVICES);
   std::lock_guard<std::mutex> lock(scratch_mu);
+  LQ_CHECK_ARG(!scratch_bound[dev] || scratch_stream[dev] == st,
+               "the static scratch of device %d is bound to stream %p, the stream of the first "
+               "lq_q8_decode_append_attn_noalloc call on it; this call is on stream %p (calls on "
+               "two streams could overlap and race on the scratch)",
+               dev, (void*)scratch_stream[dev], (void*)st);
   if (!scratch_ptr[dev]) {
     void* p = nullptr;
     LQ_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
@@ -486,6 +519,8 @@ int current_scratch(hipStream_t st, void** out) {
     if (st_clear != LQ_OK) return st_clear;
     scratch_cleared[dev] = true;
   }
+  scratch_stream[dev] = st;
+  scratch_bound[dev] = true;
   *out = scratch_ptr[dev];
   return LQ_OK;
 }

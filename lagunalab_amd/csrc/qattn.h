@@ -109,6 +109,14 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
                   const int32_t* lens, int64_t cap, DecodePlan& plan, AttnKernel& k,
                   int64_t& ws_bytes);
 
+// Workspace bytes reported to callers for such a call (-1 as attn_plan): the call's own need,
+// except that for one sequence of more than 65,536 rows with G * L <= 4 (packed kernel) it also
+// covers the dense kernel's need at 65,536 rows, the longest length that kernel serves. The
+// reported size then never falls as the length grows, so one workspace sized for a session's
+// longest length serves every shorter call of the same shape.
+int64_t attn_workspace_bytes(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t n,
+                             const int32_t* lens);
+
 
 // Per-sequence log-sum-exp merge of split partials: rows_per_seq = Hq * L partial rows per split.
 void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq,

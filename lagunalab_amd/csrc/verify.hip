@@ -17,13 +17,8 @@ extern "C" int64_t lq_verify_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv,
     set_error("unsupported verify configuration");
     return -1;
   }
-  DecodePlan plan;
-  AttnKernel k;
-  int64_t ws = 0;
-  if (attn_plan(LQ_KV_Q8, B, Hq, Hkv, L, n, nullptr, 0, plan, k, ws) < 0) {
-    set_error("bad sequence length");
-    return -1;
-  }
+  const int64_t ws = attn_workspace_bytes(LQ_KV_Q8, B, Hq, Hkv, L, n, nullptr);
+  if (ws < 0) set_error("bad sequence length");
   return ws;
 }
 

@@ -119,9 +119,11 @@ def test_python_constants_match_header():
 def test_decode_split_plan_fills_one_wave(lib):
     """The 8-bit decode plan gives each KV head at most one wave of resident workgroups (256 CUs,
     one workgroup each, over 8 KV heads: 32 splits per head), apportioned over the sequences by
-    keys per split. The split count is read back from the workspace size: the counter block plus
-    one (m, l, acc[128]) fp32 partial per split, KV head and query row. Without a GPU the host
-    assumes 256 CUs and one resident workgroup per CU."""
+    keys per split. The split count is read back from the workspace size of batches (the packed
+    kernel: the counter block plus one (m, l, acc[128]) fp32 partial per split, KV head and query
+    row) and of single sequences of at most 65,536 rows (the dense kernel: the same, then the
+    normalized q / k rows, 256-byte aligned). Without a GPU the host assumes 256 CUs and one
+    resident workgroup per CU."""
     import ctypes as C
 
     import numpy as np
@@ -132,9 +134,8 @@ def test_decode_split_plan_fills_one_wave(lib):
         arr = (C.c_int32 * len(lens))(*lens)
         ws = lib.lq_decode_workspace_bytes(8, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
         per = Hkv * (Hq // Hkv) * (128 * 4 + 8)
-        if len(lens) == 1 and lens[0] <= 65536:
-            # one short sequence: the dense kernel, whose workspace also holds the normalized q / k
-            # rows behind the partials (256-byte aligned)
+        if len(lens) == 1:
+            assert lens[0] <= 65536
             ws -= (Hq + Hkv) * 128 * 2
             return (ws - _lib.LQ_WS_ZERO_BYTES) // per
         assert (ws - _lib.LQ_WS_ZERO_BYTES) % per == 0
@@ -143,31 +144,54 @@ def test_decode_split_plan_fills_one_wave(lib):
     # config 3's lengths: a shared chunk would need 34 splits (a second, partial wave)
     c3 = [int(x) for x in np.random.default_rng(1).integers(42771, 82672, size=8)]
     assert splits(c3) == 32
-    assert splits([82671]) == 32
+    assert splits([82671, 82671]) == 32
+    assert splits([65536]) == 32
     assert splits([1000]) == 4        # at least 256 keys per split
     assert splits([1, 1, 1]) == 3     # one split per sequence at least
     assert splits([5000] * 40) == 40  # more sequences than the budget: one split each
 
 
+def _ws(lib, lens, Hq=32, Hkv=8, kind=8):
+    import ctypes as C
+    arr = (C.c_int32 * len(lens))(*lens)
+    return lib.lq_decode_workspace_bytes(kind, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
+
+
 def test_decode_kernel_choice_at_the_length_boundary(lib):
     """One sequence of up to 65,536 rows (G L <= 4) takes the dense kernel and a merge launch:
-    its workspace holds the normalized q / k rows behind the partials; from 65,537 rows, or with
-    two sequences, the packed kernel merges inside and needs only counters + partials."""
-    import ctypes as C
-
+    its workspace holds the normalized q / k rows behind the partials. From 65,537 rows the packed
+    kernel merges inside and needs only counters + partials, but the size reported for one
+    sequence also covers the dense kernel's need at 65,536 rows; batches take the packed kernel."""
     from lagunalab_amd import _lib
-
-    def ws(lens, Hq=32, Hkv=8, kind=8):
-        arr = (C.c_int32 * len(lens))(*lens)
-        return lib.lq_decode_workspace_bytes(kind, len(lens), Hq, Hkv, 128, 0, C.cast(arr, C.c_void_p))
     per = 8 * 4 * (128 * 4 + 8)  # partial bytes per split, 32q/8kv
-    packed = ws([65537])
-    assert (packed - _lib.LQ_WS_ZERO_BYTES) % per == 0 and (packed - _lib.LQ_WS_ZERO_BYTES) // per == 32
-    dense = ws([65536])
     partials = _lib.LQ_WS_ZERO_BYTES + 32 * per
+    dense = _ws(lib, [65536])
     assert dense == (partials + 255) // 256 * 256 + (32 + 8) * 128 * 2
-    two = ws([65536, 65536])
-    assert (two - _lib.LQ_WS_ZERO_BYTES) % per == 0  # a batch: packed, no norm rows
+    assert _ws(lib, [65537]) == dense and _ws(lib, [82671]) == dense
+    two = _ws(lib, [65536, 65536])
+    assert two == partials  # a batch: packed, no norm rows
     # the 4-bit and bf16 kinds always run their packed kernels
-    assert (ws([4096], kind=4) - _lib.LQ_WS_ZERO_BYTES) % per == 0
-    assert (ws([4096], kind=16) - _lib.LQ_WS_ZERO_BYTES) % per == 0
+    assert (_ws(lib, [4096], kind=4) - _lib.LQ_WS_ZERO_BYTES) % per == 0
+    assert (_ws(lib, [4096], kind=16) - _lib.LQ_WS_ZERO_BYTES) % per == 0
+
+
+@pytest.mark.parametrize("kind", [8, 4, 16])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 4), (8, 2), (48, 8), (8, 8)])
+def test_workspace_size_never_falls_as_the_length_grows(lib, kind, Hq, Hkv):
+    """A workspace sized for a session's longest length serves every shorter call of the same
+    shape: the reported size is non-decreasing in the length, across the dense/packed boundary
+    at 65,536 rows (where, with 4 KV heads or fewer, the dense plan has up to 64 splits against
+    the packed kernel's 32) and across the chunk rounding of the 4-bit and bf16 plans; the verify
+    size likewise for every block length."""
+    if kind != 8 and Hq // Hkv > 4:
+        return
+    lengths = sorted({1, 255, 256, 257, 1000, 4096, 16384, 16385, 20000, 32768, 65535, 65536,
+                      65537, 70000, 82671, 100000, 262144, 1 << 20})
+    sizes = [_ws(lib, [n], Hq, Hkv, kind) for n in lengths]
+    assert min(sizes) > 0
+    assert all(a <= b for a, b in zip(sizes, sizes[1:])), list(zip(lengths, sizes))
+    for L in (1, 2, 5):
+        if kind != 8 or (Hq // Hkv) * L > 64:
+            continue
+        vs = [lib.lq_verify_workspace_bytes(1, Hq, Hkv, L, 128, n) for n in lengths if n >= L]
+        assert all(a <= b for a, b in zip(vs, vs[1:])), (L, vs)

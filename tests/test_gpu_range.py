@@ -30,18 +30,32 @@ def _case(dev, seed, B, Hkv, n, bits, qstd, vstd, G, L):
     return kq, vq, q
 
 
+# (bits, G, B) -> the kernel that runs: one 8-bit sequence of at most 65,536 rows takes the
+# dense kernel (attn_dense.hip) whatever G; a batch of 8-bit sequences with G <= 4 takes the
+# packed kernel (qattn.hip); the 4-bit cache always takes its packed kernel (attn_q4.hip)
+DECODE_KERNELS = {(8, 4, 1): "dense", (8, 1, 1): "dense", (8, 6, 1): "dense",
+                  (8, 4, 2): "8-bit packed", (8, 1, 2): "8-bit packed", (4, 4, 1): "4-bit packed"}
+
+
 @pytest.mark.parametrize("qstd,vstd", RANGES)
-@pytest.mark.parametrize("bits,G", [(8, 4), (8, 1), (4, 4), (8, 6)])
-def test_decode_operand_range(dev, qstd, vstd, bits, G):
-    """Decode: the packed 8-bit and 4-bit kernels (G <= 4) and the dense kernel (G = 6)."""
+@pytest.mark.parametrize("bits,G,B", list(DECODE_KERNELS))
+def test_decode_operand_range(dev, qstd, vstd, bits, G, B):
+    """Decode on each kernel (DECODE_KERNELS); a batch of two sequences of 9,000 and 7,777 rows
+    for the packed 8-bit kernel, each sequence checked."""
     from lagunalab_amd.q8_attn import decode_attention
     n = 9000
-    kq, vq, q = _case(dev, int(qstd * 7 + vstd * 13) % 1000 + G + bits, 1, 8, n, bits, qstd,
-                      vstd, G, 1)
-    got = decode_attention(to_dev_bf16(q, dev), kq, vq, n=n, scale=128 ** -0.5)
+    lens = [n, 7777][:B]
+    kq, vq, q = _case(dev, int(qstd * 7 + vstd * 13) % 1000 + G + bits + 100 * B, B, 8, n, bits,
+                      qstd, vstd, G, 1)
+    got = decode_attention(to_dev_bf16(q, dev), kq, vq, lens=lens, scale=128 ** -0.5)
     assert torch.isfinite(got.float()).all()
-    want = A.fused_attention(q, cache_np(kq), cache_np(vq), n, 128 ** -0.5, bits=bits)
-    assert_attn_close(got, want, f"{bits}-bit G={G} q std {qstd} V std {vstd}", 2e-3 * vstd, RTOL)
+    for b in range(B):
+        sl = slice(b, b + 1)
+        want = A.fused_attention(q[sl], cache_np(tuple(t[sl] for t in kq)),
+                                 cache_np(tuple(t[sl] for t in vq)), lens[b], 128 ** -0.5,
+                                 bits=bits)
+        assert_attn_close(got[sl], want, f"{DECODE_KERNELS[bits, G, B]} {bits}-bit G={G} "
+                          f"sequence {b} q std {qstd} V std {vstd}", 2e-3 * vstd, RTOL)
 
 
 @pytest.mark.parametrize("qstd,vstd", RANGES)
@@ -56,15 +70,18 @@ def test_verify_operand_range(dev, qstd, vstd):
     assert_attn_close(got, want, f"verify q std {qstd} V std {vstd}", 2e-3 * vstd, RTOL)
 
 
-def test_v_scales_changing_across_the_cache(dev):
+@pytest.mark.parametrize("B", [1, 2], ids=["dense", "packed"])
+def test_v_scales_changing_across_the_cache(dev, B):
     """V groups whose scales jump by 2^10 and 2^20 between 700-row regions of the cache: the P.V
     factor is re-chosen up and down as a wave's super-tiles cross the regions (rescaling what it
     accumulated). The keys of the smallest-scale region get the largest scores, so the output
-    rests on the values that are 2^20 below the others."""
+    rests on the values that are 2^20 below the others. One sequence runs the dense kernel; a
+    batch of two (the same cache contents, 12,000 and 10,650 rows) the packed 8-bit kernel."""
     from lagunalab_amd.q8_attn import decode_attention
     from lagunalab_amd.quant import quantize_into
     rng = np.random.default_rng(77)
     n, cap, Hkv, G = 12000, 12288, 8, 4
+    lens = [n, 10650][:B]
     region = (np.arange(n) // 700) % 3  # V std 1, 2^-20, 2^-10
     # the G query heads of a KV head: one direction plus a little noise
     q = Q.randn_bf16(rng, (1, Hkv, 1, 1, 128)) * np.float32(4.0)
@@ -76,13 +93,20 @@ def test_v_scales_changing_across_the_cache(dev):
                                                  ).astype(np.float32)[None, None, :, None]
     caches = []
     for x in (k, v):
-        c = (torch.zeros((1, Hkv, cap, 128), dtype=torch.uint8, device=dev),
-             torch.zeros((1, Hkv, cap, 2), dtype=torch.bfloat16, device=dev),
-             torch.zeros((1, Hkv, cap, 2), dtype=torch.bfloat16, device=dev))
-        quantize_into(to_dev_bf16(Q.round_bf16(x), dev), *c, 0, 64, 8)
+        c = (torch.zeros((B, Hkv, cap, 128), dtype=torch.uint8, device=dev),
+             torch.zeros((B, Hkv, cap, 2), dtype=torch.bfloat16, device=dev),
+             torch.zeros((B, Hkv, cap, 2), dtype=torch.bfloat16, device=dev))
+        xb = np.repeat(Q.round_bf16(x), B, axis=0)
+        quantize_into(to_dev_bf16(xb, dev), *c, 0, 64, 8)
         caches.append(c)
-    got = decode_attention(to_dev_bf16(q, dev), caches[0], caches[1], n=n, scale=128 ** -0.5)
-    want = A.fused_attention(q, cache_np(caches[0]), cache_np(caches[1]), n, 128 ** -0.5)
-    mag = float(np.abs(want).max())
-    assert mag < 2.0 ** -14, mag  # the output is the small-scale region's
-    assert_attn_close(got, want, "V scales jumping by 2^10 and 2^20", 2e-3 * mag, RTOL)
+    qb = np.repeat(q, B, axis=0)
+    got = decode_attention(to_dev_bf16(qb, dev), caches[0], caches[1], lens=lens,
+                           scale=128 ** -0.5)
+    for b in range(B):
+        sl = slice(b, b + 1)
+        want = A.fused_attention(q, cache_np(tuple(t[sl] for t in caches[0])),
+                                 cache_np(tuple(t[sl] for t in caches[1])), lens[b], 128 ** -0.5)
+        mag = float(np.abs(want).max())
+        assert mag < 2.0 ** -14, mag  # the output is the small-scale region's
+        assert_attn_close(got[sl], want, f"V scales jumping by 2^10 and 2^20, sequence {b}",
+                          2e-3 * mag, RTOL)

@@ -9,7 +9,12 @@ reference's synthetic inputs, ``scripts/micro_kv_decode.py:30-40``), against the
 * a ragged batch at the eight lengths of ``default_rng(1).integers(42771, 82672, 8)``: the
   80,695-row sequence against the unfused path, the 44,161-row one against the fused-arithmetic
   oracle;
-* the 4-bit decode at 82,671 rows against the unfused 4-bit path.
+* the 4-bit decode at 82,671 rows against the unfused 4-bit path;
+* Laguna's own 48q/8kv shape (6 query heads per KV head: the dense kernel with the append inside,
+  then the merge launch) over 16 consecutive fused steps from 82,671 cached rows, every appended
+  row bit-exact and three sampled outputs against the unfused path, and single fused steps at
+  8,192 and 32,768 rows (the reference micro-benchmark's other contexts,
+  ``scripts/micro_kv_decode.py:19,33``).
 
 Inputs are drawn on the GPU (torch generator, fixed seeds) and copied to the host for the oracle.
 """
@@ -109,3 +114,65 @@ def test_q4_session_length_against_oracle(dev):
                                bits=4)
     assert_attn_close(got, want, "4-bit decode at 82,671 rows")
 
+
+
+STEPS48, SAMPLES48 = 16, (0, 7, 15)
+
+
+def _fused_steps(dev, g, n0, steps, hq, samples):
+    """`steps` consecutive fused decode steps of hq query heads over 8 KV heads from n0 cached
+    rows; returns the host copies of the final cache, the appended rows, q and sampled outputs."""
+    from lagunalab_amd.q8_attn import decode_append_attention
+    cap = (n0 + steps + 255) // 256 * 256
+    kq, vq = _gpu_cache(dev, g, 1, 8, n0, cap)
+    knew = torch.randn((steps, 1, 8, 1, 128), device=dev, generator=g).to(torch.bfloat16)
+    vnew = torch.randn((steps, 1, 8, 1, 128), device=dev, generator=g).to(torch.bfloat16)
+    qs = torch.randn((steps, 1, hq, 1, 128), device=dev, generator=g).to(torch.bfloat16)
+    outs = {}
+    for j in range(steps):
+        o = decode_append_attention(qs[j], knew[j], vnew[j], kq, vq, n=n0 + j, scale=SCALE)
+        if j in samples:
+            outs[j] = o
+    torch.cuda.synchronize()
+    return {"n0": n0, "k": cache_np(kq), "v": cache_np(vq), "knew": knew.float().cpu().numpy(),
+            "vnew": vnew.float().cpu().numpy(), "q": qs.float().cpu().numpy(),
+            "out": {j: o.float().cpu().numpy() for j, o in outs.items()}}
+
+
+def _check_appended(s, steps):
+    n0 = s["n0"]
+    for name, new in (("k", s["knew"]), ("v", s["vnew"])):
+        codes, scales, biases = s[name]
+        rows = new[:, 0, :, 0, :].transpose(1, 0, 2)  # [Hkv, steps, D]
+        wc, ws, wb = Q.quantize_packed(rows, 64, 8)
+        np.testing.assert_array_equal(codes[0, :, n0:n0 + steps], wc, err_msg=f"{name} codes")
+        np.testing.assert_array_equal(scales[0, :, n0:n0 + steps], ws, err_msg=f"{name} scales")
+        np.testing.assert_array_equal(biases[0, :, n0:n0 + steps], wb, err_msg=f"{name} biases")
+
+
+@pytest.fixture(scope="module")
+def laguna_session():
+    dev = torch.device("cuda", 0)
+    return _fused_steps(dev, torch.Generator(device=dev).manual_seed(4848), N0, STEPS48, 48,
+                        SAMPLES48)
+
+
+def test_laguna_shape_steps_append_bit_exact_rows(laguna_session):
+    _check_appended(laguna_session, STEPS48)
+
+
+@pytest.mark.parametrize("j", SAMPLES48)
+def test_laguna_shape_step_output_matches_unfused_oracle(laguna_session, j):
+    s = laguna_session
+    n = N0 + j + 1
+    want = A.unfused_attention(s["q"][j], s["k"], s["v"], n, SCALE)
+    assert_attn_close(s["out"][j], want, f"48q/8kv fused step {j} at n={n}")
+
+
+@pytest.mark.parametrize("n0", [8191, 32767])
+def test_laguna_shape_single_step_at_reference_contexts(dev, n0):
+    """One 48q/8kv fused step that leaves 8,192 / 32,768 rows in the cache."""
+    s = _fused_steps(dev, torch.Generator(device=dev).manual_seed(n0), n0, 1, 48, (0,))
+    _check_appended(s, 1)
+    want = A.unfused_attention(s["q"][0], s["k"], s["v"], n0 + 1, SCALE)
+    assert_attn_close(s["out"][0], want, f"48q/8kv fused step at n={n0 + 1}")
