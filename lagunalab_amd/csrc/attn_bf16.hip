@@ -264,7 +264,8 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below
-  packed_finish<BW>(oacc, m_run, lsum, 0.0f, 0.0f, 1.0f, &sm.acc[0][0][0], &sm.st[0][0][0],
+  const float osc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  packed_finish<BW>(oacc, m_run, lsum, 0.0f, 0.0f, osc, &sm.acc[0][0][0], &sm.st[0][0][0],
                     &sh_last, args, plan, x, b, hk, R);
 }
 

@@ -144,6 +144,18 @@ __device__ __forceinline__ void vscale_apply(float a0, float a1, VScale& v, f4_t
   v.f1 = n1 == VK_NONE ? 0.0f : pow2f(n1);
 }
 
+// The packed finish's per-wave output factors: base * 2^-kv of the dim's quant group, times `odd`
+// for odd dims in the 4-bit layout (class 2 g + (dim & 1)); applied to the summed accumulators
+// instead of rescaling each accumulator before the finish (exact: powers of two).
+__device__ __forceinline__ void vscale_out(const VScale& v, float base, float odd, float (&osc)[4]) {
+  const float i0 = v.k0 == VK_NONE ? base : base * pow2f(-v.k0);
+  const float i1 = v.k1 == VK_NONE ? base : base * pow2f(-v.k1);
+  osc[0] = i0;
+  osc[1] = i0 * odd;
+  osc[2] = i1;
+  osc[3] = i1 * odd;
+}
+
 // Takes the P.V factors back out of the accumulators (before the epilogue).
 template <int NACC = 1>
 __device__ __forceinline__ void vscale_remove(const VScale& v, f4_t* oacc) {
@@ -229,6 +241,14 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two consecutive floats (8-byte aligned) read at the device-coherent level: one 8-byte
+// agent-scope load (global_load_dwordx2 sc1), which no stale line of this XCD's L2 can serve, so
+// a reader needs no cache invalidation before it. Loads of a batch go out together.
+__device__ __forceinline__ float2 ld_agent2(const float* p) {
+  const uint64_t u = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
 __device__ __forceinline__ float ld_agent(const float* p) {
   return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -261,14 +281,20 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
   float M = -INFINITY, den = 0.0f;
   float a[4] = {0.f, 0.f, 0.f, 0.f};
   if (row < R) {
+    // this thread's partials of split s0 (64-bit base once), later splits at 32-bit offsets
+    // (so the loads go out back to back, with no 64-bit multiply per split in front of them)
+    const int64_t pr0 = (int64_t)s0 * rs + r0 + row;
+    const float2* __restrict__ mlp = part_ml + pr0;
+    const float* __restrict__ accp = part_acc + pr0 * D + d0;
+    const int step = (int)rs;
     for (int base = par; base < ns; base += NPAR * MCH) {
       float mv[MCH], lv[MCH], av[MCH][4];
 #pragma unroll
       for (int k = 0; k < MCH; ++k) {
-        const int sk = min(base + NPAR * k, ns - 1);
-        const int64_t pr = (s0 + sk) * rs + r0 + row;
-        const float2 ml = part_ml[pr];
-        const float4 a4 = *reinterpret_cast<const float4*>(part_acc + pr * D + d0);
+        const int off = min(base + NPAR * k, ns - 1) * step;
+        const float2 ml = ld_agent2(reinterpret_cast<const float*>(mlp + off));
+        const float2 a01 = ld_agent2(accp + off * D), a23 = ld_agent2(accp + off * D + 2);
+        const float4 a4 = make_float4(a01.x, a01.y, a23.x, a23.y);
         mv[k] = ml.x;
         lv[k] = ml.y;
         av[k][0] = a4.x;
@@ -276,26 +302,28 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
         av[k][2] = a4.z;
         av[k][3] = a4.w;
       }
+      // Branch-free: every loaded value is used on every path, so that the compiler issues
+      // all loads of the batch before the first wait (with the weighting under a branch on the
+      // maxima it waited for the m values, then issued the acc and l loads: a second memory
+      // round trip). Splits whose rows saw no key (m = -inf) weigh 0.
       float cm = -INFINITY;
 #pragma unroll
-      for (int k = 0; k < MCH; ++k)
-        if (base + NPAR * k < ns) cm = fmaxf(cm, mv[k]);
+      for (int k = 0; k < MCH; ++k) cm = fmaxf(cm, base + NPAR * k < ns ? mv[k] : -INFINITY);
       const float Mn = fmaxf(M, cm);
-      if (Mn != -INFINITY) {
-        const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mn);
-        den *= sc;
+      const float Mr = Mn == -INFINITY ? 0.0f : Mn;
+      const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mr);
+      den *= sc;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] *= sc;
+      for (int j = 0; j < 4; ++j) a[j] *= sc;
 #pragma unroll
-        for (int k = 0; k < MCH; ++k) {
-          const bool use = base + NPAR * k < ns && mv[k] != -INFINITY;
-          const float w = use ? exp2_nonpos(mv[k] - Mn) : 0.0f;
-          den += w * lv[k];
+      for (int k = 0; k < MCH; ++k) {
+        const bool use = base + NPAR * k < ns && mv[k] != -INFINITY;
+        const float w = use ? exp2_nonpos(mv[k] - Mr) : 0.0f;
+        den = fmaf(w, lv[k], den);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) a[j] += w * av[k][j];
-        }
-        M = Mn;
+        for (int j = 0; j < 4; ++j) a[j] = fmaf(w, av[k][j], a[j]);
       }
+      M = Mn;
     }
   }
   // parity 1 hands (M, den, a) to parity 0 through LDS
@@ -330,15 +358,16 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 // Epilogue of the packed kernels. Per wave: the accumulator columns of the 4 key tiles of each
 // query row are summed (lanes 4 and 8 apart in a row), the softmax sum and the two bias sums over
 // all lanes; then the NW waves meet in LDS and their log-sum-exp merge is the workgroup's split
-// partial: acc * out_scale + bias sum of the quant group, written with agent-scope stores. The
-// LDS layout puts the NW waves' values of one quantity side by side (acc_lds [4][D][NW],
-// st_lds [4][4][NW]: m, l, bias sum 0, bias sum 1), so that each output element takes three
-// NW-wide LDS reads issued together. Then the arrival count, and the last workgroup of the
-// (sequence, KV head) merges all splits (merge_rows4). The caller has synchronised the workgroup
-// so that acc_lds/st_lds (16-byte aligned, at least 4 D NW and 16 NW floats) may overwrite its
-// tile buffers.
+// partial: acc * (the wave's output factor of the dim's class, osc) + bias sum of the quant
+// group, written with agent-scope stores. The LDS layout puts the NW waves' values of one quantity
+// side by side (acc_lds [4][D][NW], st_lds [4][4][NW]: m, l, bias sum 0, bias sum 1, then
+// [4][NW]: the output factors), so that each output element takes four NW-wide LDS reads issued
+// together. Then the arrival count, and the last workgroup of the (sequence, KV head) merges all
+// splits (merge_rows4). The caller has synchronised the workgroup so that acc_lds/st_lds (16-byte
+// aligned, at least 4 D NW and 20 NW floats) may overwrite its tile buffers.
 // EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (row) + p (the 4-bit kernel's P.V
-// operands); otherwise tile j holds dims 16 j + row.
+// operands); otherwise tile j holds dims 16 j + row. osc: output factor of dim class
+// 2 (dim / 64) + (EVEN_ODD ? dim & 1 : 0).
 template <int NW>
 struct WaveVec;
 template <>
@@ -356,7 +385,7 @@ struct WaveVec<2> {
 
 template <int NW, bool EVEN_ODD = false>
 __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bsum0, float bsum1,
-                              float out_scale, float* acc_lds, float* st_lds, int* sh_last,
+                              const float (&osc)[4], float* acc_lds, float* st_lds, int* sh_last,
                               const AttnArgs& args, const DecodePlan& plan, int x, int b, int hk,
                               int R) {
   typedef typename WaveVec<NW>::T wvec;
@@ -366,6 +395,10 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
   const int lc = lane & 15;
   const int lq4 = lane >> 4;
   const int Hkv = args.Hkv;
+  // The sums are pinned in every lane before the branch below (the empty asm): left to itself
+  // the compiler moved the adds into the branch, away from their DPP moves, and each step became
+  // three instructions (zero, DPP move, add) instead of one v_add_f32_dpp -- at one wave per SIMD
+  // that is ~1 us of issue time after the last tile.
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -373,6 +406,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
       float v = oacc[dt][r];
       v += dpp<DPP_ROW_ROR4>(v);
       v += dpp<DPP_ROW_ROR8>(v);
+      asm("" : "+v"(v));
       oacc[dt][r] = v;
     }
   float tot[3] = {lsum, bsum0, bsum1};
@@ -399,6 +433,10 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
       st_lds[(lc * 4 + 2) * NW + wv] = tot[1];
       st_lds[(lc * 4 + 3) * NW + wv] = tot[2];
     }
+    if (lane == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st_lds[(16 + c) * NW + wv] = osc[c];
+    }
   }
   __syncthreads();
   for (int o = tid; o < R * D; o += 64 * NW) {
@@ -407,6 +445,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     const int g = d >> 6;
     const wvec m = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 0) * NW);
     const wvec bs = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 2 + g) * NW);
+    const wvec os = *reinterpret_cast<const wvec*>(st_lds + (16 + 2 * g + (EVEN_ODD ? d & 1 : 0)) * NW);
     const wvec ac = *reinterpret_cast<const wvec*>(acc_lds + (col * D + d) * NW);
     float M = -INFINITY;
 #pragma unroll
@@ -416,7 +455,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     for (int w = 0; w < NW; ++w) {
       const float mw = WaveVec<NW>::get(m, w);
       const float e = mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M);
-      a += e * fmaf(WaveVec<NW>::get(ac, w), out_scale, WaveVec<NW>::get(bs, w));
+      a += e * fmaf(WaveVec<NW>::get(ac, w), WaveVec<NW>::get(os, w), WaveVec<NW>::get(bs, w));
     }
     st_agent(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
   }
@@ -460,9 +499,9 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
   }
   __syncthreads();
   if (!*sh_last) return;
-  // Acquire: drop this CU's and this XCD's cached lines so that the loads below fetch the
-  // partials the other workgroups wrote through to the device-coherent level.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // The loads of merge_rows4 are agent-scope (device-coherent level) and issued after the count
+  // returned: they see every split's partials without an acquire fence (an invalidation of the
+  // CU's and the XCD's caches, ~0.4 us on this path).
   merge_rows4<NW>(b, hk, Hkv, R, plan, args.part_acc, args.part_ml, args.out, acc_lds);
 }
 

@@ -391,11 +391,10 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     if (si + 3 < nst) issue(si + 3, B1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-  for (int t = 0; t < 4; ++t) oacc[2 * t + 1] *= 0.0625f;  // odd dims' codes entered at 16 c
-  vscale_remove(vsc, oacc);
+  float osc[4];  // output factors: 2^24 over the P.V factors, and 1/16 for the odd dims (their
+  vscale_out(vsc, 16777216.0f, 0.0625f, osc);  // codes entered as 16 c)
   __syncthreads();
-  packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.fin.acc[0][0][0],
+  packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, osc, &sm.fin.acc[0][0][0],
                           &sm.fin.st[0][0][0], &sm.fin.last, args, plan, x, b, hk, R);
 }
 

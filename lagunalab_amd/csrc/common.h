@@ -127,9 +127,16 @@ constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
 constexpr int DPP_ROW_MIRROR = 0x140;       // lane i of a row <- lane 15 - i
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i of a half row <- lane 7 - i
 
+// x of another lane of the same row of 16. Only controls under which every lane reads a valid
+// source lane (quad_perm, row_ror, the mirrors), so the DPP "old" value is never used: it is left
+// undefined, which lets the compiler fold the move into the VALU op that consumes it
+// (v_add_f32_dpp, v_max_f32_dpp, ...). With an explicit old value each use was three instructions
+// (v_mov of the old value, v_mov_b32_dpp, the op), a latency chain in the reductions.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+  static_assert(CTRL <= 0xFF || (CTRL >= 0x121 && CTRL <= 0x12F) || CTRL == 0x140 || CTRL == 0x141,
+                "dpp: only full permutations within a row (no shifts or broadcasts)");
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 // Max / sum with the lane 16 (32) apart, on the VALU: v_permlane16_swap (v_permlane32_swap)

@@ -543,9 +543,10 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     }
   }
 
-  vscale_remove(vsc, oacc);
+  float osc[4];  // output factors: 2^24 (codes entered as c 2^-24) over the P.V factors
+  vscale_out(vsc, 16777216.0f, 1.0f, osc);
   __syncthreads();  // every wave is done with its LDS tiles before they are reused below
-  packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, 16777216.0f, &sm.acc[0][0][0],
+  packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, osc, &sm.acc[0][0][0],
                        &sm.st[0][0][0], &sh_last, args, plan, x, b, hk, R);
 }
 
