@@ -33,7 +33,10 @@
 //    copies may have read the rows before or while they were stored), once an LDS count says the
 //    staging waves are done. No other wave uses those rows. Same arithmetic as
 //    quantize_group_kernel, so the codes agree.
-//  * Partials (m, l, acc) per (workgroup, query row) go to the workspace; decode_merge_kernel
+//  * Partials (m, l, acc) per (workgroup, query row) go to the workspace. With MERGE (at most 8
+//    rows per KV head: decode of one sequence, up to 16 splits x 8 rows x 520 B = 66 KB per head)
+//    they are written with agent-scope stores and the last workgroup of (sequence, KV head) to
+//    arrive merges them (merge_rows4), as the packed kernels do; otherwise decode_merge_kernel
 //    merges them (at 16+ rows per KV head the partials of 32 workgroups are ~330 KB per head, too
 //    much for one workgroup to merge at the end of the attention kernel).
 #include "attn_dev.h"
@@ -89,7 +92,7 @@ __device__ __forceinline__ void dma_b32_v(const void* g, uint32_t lds) {
                :: "v"(g), "s"(lds) : "memory");
 }
 
-template <int NT, bool CAUSAL, int ST, int DW>
+template <int NT, bool CAUSAL, int ST, int DW, bool MERGE>
 __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args, DecodePlan plan) {
   static_assert(ST == 32 || ST == 64, "super-tiles of 32 or 64 keys");
   constexpr int MT = ST / 16;  // M tiles (16 keys) per super-tile
@@ -101,6 +104,8 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   using DenseTerms = lq::DenseTerms<ST>;
   constexpr int DST = ST;
   __shared__ DenseSmem<NT, ST, DW> sm;
+  __shared__ int sh_last;
+  static_assert(!MERGE || (NT == 1 && DW == 8), "in-kernel merge: one N tile on 8 waves");
   const uint16_t* __restrict__ q = args.q;
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
@@ -658,8 +663,13 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
       for (int r = 0; r < 4; ++r) a[r] += e * fmaf(v[r], 16777216.0f, bias);
     }
     const int d0 = 16 * dt + 4 * (ln >> 4);
-    *reinterpret_cast<f4_t*>(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D +
-                             d0) = a;
+    float* pa = args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d0;
+    if constexpr (MERGE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st_agent(pa + r, a[r]);
+    } else {
+      *reinterpret_cast<f4_t*>(pa) = a;
+    }
   }
   if (tid < R) {
     const int col = tid;
@@ -672,28 +682,58 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
       const float* st = sm.st[w][col];
       l += st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M) * st[1];
     }
-    args.part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
+    float2* pml = args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col;
+    if constexpr (MERGE) {
+      st_agent(reinterpret_cast<float*>(pml), M);
+      st_agent(reinterpret_cast<float*>(pml) + 1, l);
+    } else {
+      *pml = make_float2(M, l);
+    }
+  }
+  if constexpr (MERGE) {
+    // Every thread's partial stores have completed (vmcnt 0) before the barrier in front of the
+    // arrival count; the last workgroup of (sequence, KV head) merges all splits (agent-scope
+    // loads issued after its count returned) and resets the counter for the next call.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t* c = arrival_counter(args.counters, b * Hkv + hk);
+      const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
+      const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev + 1 == ns;
+      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sh_last = last;
+    }
+    __syncthreads();
+    if (!sh_last) return;
+    float* red = reinterpret_cast<float*>(&sm.acc[0][0][0]);  // free: the wave partials are read
+    if (R <= 4)
+      merge_rows4<DW, 4>(b, hk, Hkv, R, plan, args.part_acc, args.part_ml, args.out, red);
+    else
+      merge_rows4<DW, 8>(b, hk, Hkv, R, plan, args.part_acc, args.part_ml, args.out, red);
   }
 }
 
 }  // namespace
 
 // Up to 32 query rows per KV head: 32-key super-tiles on 8 waves. More rows: 64-key super-tiles
-// on 4 waves (their accumulators leave no registers for a second wave per SIMD).
-QAttnFn q8_dense_attn_fn(int nt, bool causal) {
+// on 4 waves (their accumulators leave no registers for a second wave per SIMD). merge: the
+// in-kernel split merge (decode, at most 8 rows per KV head).
+QAttnFn q8_dense_attn_fn(int nt, bool causal, bool merge) {
+  if (merge) return nt == 1 && !causal ? q8_attn_dense_kernel<1, false, 32, 8, true> : nullptr;
   if (causal) {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, true, 32, 8>;
-      case 2: return q8_attn_dense_kernel<2, true, 32, 8>;
-      case 3: return q8_attn_dense_kernel<3, true, 64, 4>;
-      case 4: return q8_attn_dense_kernel<4, true, 64, 4>;
+      case 1: return q8_attn_dense_kernel<1, true, 32, 8, false>;
+      case 2: return q8_attn_dense_kernel<2, true, 32, 8, false>;
+      case 3: return q8_attn_dense_kernel<3, true, 64, 4, false>;
+      case 4: return q8_attn_dense_kernel<4, true, 64, 4, false>;
     }
   } else {
     switch (nt) {
-      case 1: return q8_attn_dense_kernel<1, false, 32, 8>;
-      case 2: return q8_attn_dense_kernel<2, false, 32, 8>;
-      case 3: return q8_attn_dense_kernel<3, false, 64, 4>;
-      case 4: return q8_attn_dense_kernel<4, false, 64, 4>;
+      case 1: return q8_attn_dense_kernel<1, false, 32, 8, false>;
+      case 2: return q8_attn_dense_kernel<2, false, 32, 8, false>;
+      case 3: return q8_attn_dense_kernel<3, false, 64, 4, false>;
+      case 4: return q8_attn_dense_kernel<4, false, 64, 4, false>;
     }
   }
   return nullptr;

@@ -254,30 +254,34 @@ __device__ __forceinline__ float ld_agent(const float* p) {
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// Log-sum-exp merge of the split partials of sequence b, KV head hk (R <= 4 query rows) by one
-// workgroup, into the output rows (b * Hkv + hk) * R + row of out [B, Hq, L, D] (bf16).
-// Partial (m, l, acc) of split s, row r: part_ml / part_acc at (s * Hkv + hk) * R + r.
-// Thread t takes 4 dims (t % 32) of row (t % 128) / 32 over the splits of parity t / 128 (two
-// parities with 4 waves, one with 2): it loads (m, l, acc) of up to MCH splits at once (one
-// memory round trip for up to MCH splits per parity), merges them with its own running max, and
-// the parities meet in LDS. red: LDS scratch of at least 768 floats.
-constexpr int MCH = 16;
-template <int NW>
+// Log-sum-exp merge of the split partials of sequence b, KV head hk (R <= RW query rows, RW = 4
+// or 8) by one workgroup of NW waves, into the output rows (b * Hkv + hk) * R + row of
+// out [B, Hq, L, D] (bf16). Partial (m, l, acc) of split s, row r: part_ml / part_acc at
+// (s * Hkv + hk) * R + r.
+// Thread t takes 4 dims (t % 32) of row (t % 32 RW) / 32 over the splits of parity t / 32 RW (one
+// to four parities: NW * 64 / (32 RW)): it loads (m, l, acc) of up to MCH splits at once (one
+// memory round trip for up to MCH splits per parity: 16 with one or two parities, 8 with four),
+// merges them with its own running max, and the parities meet in LDS. red: LDS scratch of at
+// least 6 * 32 RW * max(1, parities - 1) floats.
+template <int NW, int RW = 4>
 __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& plan,
                             const float* __restrict__ part_acc,
                             const float2* __restrict__ part_ml, uint16_t* __restrict__ out,
                             float* red) {
-  constexpr int NPAR = NW / 2;  // split parities (128 threads each)
-  static_assert(NPAR == 1 || NPAR == 2, "merge_rows4 runs on 2 or 4 waves");
+  constexpr int TPR = 32 * RW;         // threads per parity
+  constexpr int NPAR = 64 * NW / TPR;  // split parities
+  static_assert(RW == 4 || RW == 8, "4 or 8 rows per parity");
+  static_assert(NPAR == 1 || NPAR == 2 || NPAR == 4, "one, two or four split parities");
+  constexpr int MCH = NPAR == 4 ? 8 : 16;
   const int tid = threadIdx.x;
   const int s0 = plan.split_begin[b];
   const int ns = plan.split_begin[b + 1] - s0;
   const int64_t rs = (int64_t)Hkv * R;
   const int64_t r0 = (int64_t)hk * R;
-  const int o = tid & 127;
+  const int o = tid % TPR;
   const int row = o >> 5;
   const int d0 = 4 * (o & 31);
-  const int par = tid >> 7;
+  const int par = tid / TPR;
   float M = -INFINITY, den = 0.0f;
   float a[4] = {0.f, 0.f, 0.f, 0.f};
   if (row < R) {
@@ -326,20 +330,52 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
       M = Mn;
     }
   }
+  if constexpr (NPAR == 4) {
+    // parities 1-3 hand (M, den, a) to parity 0 through LDS; one log-sum-exp over the four
+    if (par > 0) {
+      float* r = red + 6 * TPR * (par - 1);
+      r[o] = M;
+      r[TPR + o] = den;
+      *reinterpret_cast<float4*>(r + 2 * TPR + 4 * o) = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    __syncthreads();
+    if (par == 0 && row < R) {
+      float Mp[4] = {M, red[o], red[6 * TPR + o], red[12 * TPR + o]};
+      const float Mx = fmaxf(fmaxf(Mp[0], Mp[1]), fmaxf(Mp[2], Mp[3]));
+      float num[4] = {0.f, 0.f, 0.f, 0.f}, dsum = 0.0f;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float e = Mp[p] == -INFINITY ? 0.0f : exp2_nonpos(Mp[p] - Mx);
+        const float dp = p == 0 ? den : red[6 * TPR * (p - 1) + TPR + o];
+        const float4 ap = p == 0 ? make_float4(a[0], a[1], a[2], a[3])
+                                 : *reinterpret_cast<const float4*>(red + 6 * TPR * (p - 1) + 2 * TPR + 4 * o);
+        dsum = fmaf(e, dp, dsum);
+        num[0] = fmaf(e, ap.x, num[0]);
+        num[1] = fmaf(e, ap.y, num[1]);
+        num[2] = fmaf(e, ap.z, num[2]);
+        num[3] = fmaf(e, ap.w, num[3]);
+      }
+      const float inv = 1.0f / dsum;
+      const uint32_t lo = (uint32_t)f32_to_bf16(num[0] * inv) | ((uint32_t)f32_to_bf16(num[1] * inv) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(num[2] * inv) | ((uint32_t)f32_to_bf16(num[3] * inv) << 16);
+      *reinterpret_cast<uint2*>(out + (((int64_t)b * Hkv + hk) * R + row) * D + d0) = make_uint2(lo, hi);
+    }
+    return;
+  }
   // parity 1 hands (M, den, a) to parity 0 through LDS
   float M1 = -INFINITY, den1 = 0.0f;
   float4 a1 = make_float4(0.f, 0.f, 0.f, 0.f);
   if (NPAR == 2) {
     if (par == 1) {
       red[o] = M;
-      red[128 + o] = den;
-      *reinterpret_cast<float4*>(red + 256 + 4 * o) = make_float4(a[0], a[1], a[2], a[3]);
+      red[TPR + o] = den;
+      *reinterpret_cast<float4*>(red + 2 * TPR + 4 * o) = make_float4(a[0], a[1], a[2], a[3]);
     }
     __syncthreads();
     if (par == 0) {
       M1 = red[o];
-      den1 = red[128 + o];
-      a1 = *reinterpret_cast<const float4*>(red + 256 + 4 * o);
+      den1 = red[TPR + o];
+      a1 = *reinterpret_cast<const float4*>(red + 2 * TPR + 4 * o);
     }
   }
   if (par == 0 && row < R) {

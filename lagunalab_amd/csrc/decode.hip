@@ -194,6 +194,11 @@ bool q8_packed(int64_t R, int64_t B, int64_t longest) {
   return R <= 4 && !(B == 1 && longest <= DENSE_BELOW);
 }
 
+// Decode on the dense kernel with at most 8 rows per KV head merges its splits in the kernel (at
+// most 32 splits x 8 rows of partials per KV head for the last workgroup to read) instead of a
+// decode_merge_kernel launch.
+bool dense_merges(int64_t R, int64_t L) { return L == 1 && R <= 8; }
+
 // Decode with the dense kernel: where the q and new K rows after q/k norm + RoPE go in the
 // workspace (behind the partials, 256-byte aligned).
 int64_t norm_rows_offset(int64_t partials_end) { return (partials_end + 255) / 256 * 256; }
@@ -211,26 +216,28 @@ int64_t attn_plan(int kind, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64
   }
   if (kind == LQ_KV_Q8) {
     const int nt = (int)((R + 15) / 16);
-    if (q8_packed(R, B, longest))
-      k = {q8_attn_fn(L > 1), 256, true};
-    else
-      k = {q8_dense_attn_fn(nt, L > 1), q8_dense_threads(nt), false};
+    if (q8_packed(R, B, longest)) {
+      k = {q8_attn_fn(L > 1), 256, true, true};
+    } else {
+      const bool merge = dense_merges(R, L);
+      k = {q8_dense_attn_fn(nt, L > 1, merge), q8_dense_threads(nt), merge, false};
+    }
   } else if (kind == LQ_KV_BF16 && R <= 4) {
-    k = {bf16_attn_fn(L > 1), 128, true};
+    k = {bf16_attn_fn(L > 1), 128, true, true};
   } else if (kind == LQ_KV_Q4 && R <= 4) {
-    k = {q4_attn_fn(L > 1), 256, true};
+    k = {q4_attn_fn(L > 1), 256, true, true};
   } else {
     return -1;
   }
   if (!k.fn) return -1;
   if (B * Hkv > MAX_COUNTERS) return -1;
-  // One workgroup per CU for the dense kernel too (its 8 or 4 waves hold about 150 KB of LDS).
-  const int per_cu = k.merges ? attn_occupancy(k.fn, k.threads) : 1;
+  // One workgroup per CU for the dense kernel (its 8 or 4 waves hold about 150 KB of LDS).
+  const int per_cu = k.packed ? attn_occupancy(k.fn, k.threads) : 1;
   const int64_t S = make_plan(B, Hkv, n, lens, cap, per_cu * device_cu_count(),
                               kind == LQ_KV_Q8, k.merges ? MAX_SPLITS : MERGE_SPLITS, plan);
   if (S < 0) return -1;
   ws_bytes = WS_COUNTER_BYTES + S * Hkv * R * (int64_t)(D * sizeof(float) + sizeof(float2));
-  if (kind == LQ_KV_Q8 && L == 1 && !k.merges)  // normalized q / k rows (norm entry)
+  if (kind == LQ_KV_Q8 && L == 1 && !k.packed)  // normalized q / k rows (norm entry)
     ws_bytes = norm_rows_offset(ws_bytes) + B * (Hq + Hkv) * D * (int64_t)sizeof(uint16_t);
   return S;
 }
@@ -315,10 +322,11 @@ int decode_attn(int kind, const uint16_t* q, void* kc, uint16_t* ks, uint16_t* k
     return LQ_EWORKSPACE;
   }
   const bool fused_merge = kern.merges;
+  const bool packed = kern.packed;
   LQ_CHECK_ARG(!pos_dev || (kind == LQ_KV_Q8 && k_new),
                "device positions need the fused 8-bit append");
   LQ_CHECK_ARG(!norm || (kind == LQ_KV_Q8 && k_new), "the q/k norm needs the fused 8-bit append");
-  if (norm && !fused_merge) {
+  if (norm && !packed) {
     // Dense kernel (more than 4 query heads per KV head): q/k RMSNorm + RoPE as a launch of its
     // own (the same arithmetic as the packed kernel's prologue) into the workspace, at the append
     // row (device positions, or n - 1), then the fused step from those rows.

@@ -84,9 +84,10 @@ struct NormArgs {
 // Launches the decode variant (no causal mask) with the in-kernel q/k norm on an S x Hkv grid.
 void launch_q8_attn_norm(unsigned S, unsigned Hkv, hipStream_t st, const AttnArgs& a,
                          const DecodePlan& plan, const NormArgs& nargs);
-// Dense-layout kernel (attn_dense.hip) for 4 < G * L <= 16 nt rows per KV head; partials merged
-// by decode_merge_kernel.
-QAttnFn q8_dense_attn_fn(int nt, bool causal);
+// Dense-layout kernel (attn_dense.hip) for 4 < G * L <= 16 nt rows per KV head, and for up to 4
+// over one sequence of at most 65,536 rows; partials merged by decode_merge_kernel, or (merge:
+// decode with at most 8 rows per KV head, nt = 1) by the kernel's last workgroup per KV head.
+QAttnFn q8_dense_attn_fn(int nt, bool causal, bool merge);
 // Its workgroup size for nt column tiles.
 int q8_dense_threads(int nt);
 
@@ -95,6 +96,8 @@ struct AttnKernel {
   QAttnFn fn;
   int threads;
   bool merges;  // the kernel merges the split partials itself (else decode_merge_kernel does)
+  bool packed;  // a packed kernel (8-bit, 4-bit, bf16): at most 4 rows per KV head, one or more
+                // workgroups per CU; else the dense kernel (one workgroup per CU)
 };
 
 // Plain-bf16 cache kernel (attn_bf16.hip), G * L <= 4.

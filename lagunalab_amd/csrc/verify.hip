@@ -54,7 +54,7 @@ int verify_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
               (long long)need);
     return LQ_EWORKSPACE;
   }
-  const bool packed = kern.merges;
+  const bool packed = kern.packed;
   AttnArgs a{};
   a.q = q;
   a.kc = kc;
@@ -83,7 +83,7 @@ int verify_attn(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
   hipLaunchKernelGGL(kern.fn, dim3((unsigned)S, (unsigned)Hkv), dim3((unsigned)kern.threads), 0,
                      st, a, plan);
   LQ_CHECK_LAUNCH("q8 attention kernel");
-  if (!packed) {
+  if (!kern.merges) {
     launch_merge(a.part_acc, a.part_ml, (int)(Hq * L), plan, B, out, st);
     LQ_CHECK_LAUNCH("decode_merge_kernel");
   }
