@@ -34,7 +34,7 @@ struct Bf16Buf {
 struct Bf16Smem {
   union {
     Bf16Buf buf[BW][2];
-    alignas(16) float acc[BW][4][D];
+    alignas(16) float acc[BW][4][FIN_ROW];
   };
   alignas(16) float st[BW][4][6];
   alignas(16) uint8_t qstage[BW][4 * D * 2];  // each wave's copy of the (<= 4) q rows

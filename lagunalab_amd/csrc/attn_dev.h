@@ -241,6 +241,17 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two consecutive floats (8-byte aligned) as one 8-byte agent-scope store.
+__device__ __forceinline__ void st_agent2(float* p, float lo, float hi) {
+  const uint64_t u = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Four consecutive floats (16-byte aligned) read at the device-coherent level with one 16-byte
+// load (buffer_load_dwordx4 sc1, the cache policy of an agent-scope load): `rsrc` covers the
+// buffer, `off` is the byte offset in it.
+__device__ __forceinline__ f4_t ld_agent4(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 16);
+}
 // Two consecutive floats (8-byte aligned) read at the device-coherent level: one 8-byte
 // agent-scope load (global_load_dwordx2 sc1), which no stale line of this XCD's L2 can serve, so
 // a reader needs no cache invalidation before it. Loads of a batch go out together.
@@ -289,7 +300,11 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
     // (so the loads go out back to back, with no 64-bit multiply per split in front of them)
     const int64_t pr0 = (int64_t)s0 * rs + r0 + row;
     const float2* __restrict__ mlp = part_ml + pr0;
-    const float* __restrict__ accp = part_acc + pr0 * D + d0;
+    // the acc partials of the sequence's splits through one buffer resource (wave-uniform base:
+    // the sequence's first split), this thread's 16 bytes at a 32-bit byte offset
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(part_acc + (int64_t)s0 * rs * D), 0, 0x7fffffff, 0x00020000);
+    const uint32_t abase = (uint32_t)(((r0 + row) * D + d0) * 4);
     const int step = (int)rs;
     for (int base = par; base < ns; base += NPAR * MCH) {
       float mv[MCH], lv[MCH], av[MCH][4];
@@ -297,14 +312,13 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
       for (int k = 0; k < MCH; ++k) {
         const int off = min(base + NPAR * k, ns - 1) * step;
         const float2 ml = ld_agent2(reinterpret_cast<const float*>(mlp + off));
-        const float2 a01 = ld_agent2(accp + off * D), a23 = ld_agent2(accp + off * D + 2);
-        const float4 a4 = make_float4(a01.x, a01.y, a23.x, a23.y);
+        const f4_t a4 = ld_agent4(rsrc, abase + (uint32_t)off * (D * 4));
         mv[k] = ml.x;
         lv[k] = ml.y;
-        av[k][0] = a4.x;
-        av[k][1] = a4.y;
-        av[k][2] = a4.z;
-        av[k][3] = a4.w;
+        av[k][0] = a4[0];
+        av[k][1] = a4[1];
+        av[k][2] = a4[2];
+        av[k][3] = a4[3];
       }
       // Branch-free: every loaded value is used on every path, so that the compiler issues
       // all loads of the batch before the first wait (with the weighting under a branch on the
@@ -395,15 +409,18 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 // query row are summed (lanes 4 and 8 apart in a row), the softmax sum and the two bias sums over
 // all lanes; then the NW waves meet in LDS and their log-sum-exp merge is the workgroup's split
 // partial: acc * (the wave's output factor of the dim's class, osc) + bias sum of the quant
-// group, written with agent-scope stores. The LDS layout puts the NW waves' values of one quantity
-// side by side (acc_lds [4][D][NW], st_lds [4][4][NW]: m, l, bias sum 0, bias sum 1, then
-// [4][NW]: the output factors), so that each output element takes four NW-wide LDS reads issued
-// together. Then the arrival count, and the last workgroup of the (sequence, KV head) merges all
-// splits (merge_rows4). The caller has synchronised the workgroup so that acc_lds/st_lds (16-byte
-// aligned, at least 4 D NW and 20 NW floats) may overwrite its tile buffers.
-// EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (row) + p (the 4-bit kernel's P.V
-// operands); otherwise tile j holds dims 16 j + row. osc: output factor of dim class
-// 2 (dim / 64) + (EVEN_ODD ? dim & 1 : 0).
+// group, written with agent-scope stores. LDS layout: acc_lds [NW][4 rows][FIN_ROW] (a wave's row
+// of D floats, padded by 16 bytes so that the four rows' 16-byte writes of one instruction fall in
+// different banks: each lane holding a row writes its dims with 8 ds_write_b128), st_lds
+// [4][4][NW]: m, l, bias sum 0, bias sum 1 of each wave side by side, then [4][NW]: the output
+// factors. Each output pair of dims then takes NW 8-byte reads and three NW-wide reads. Then the
+// arrival count, and the last workgroup of the (sequence, KV head) merges all splits
+// (merge_rows4). The caller has synchronised the workgroup so that acc_lds/st_lds (16-byte
+// aligned, at least 4 FIN_ROW NW and 20 NW floats) may overwrite its tile buffers.
+// EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (4 lane group + r) + p (the 4-bit
+// kernel's P.V operands); otherwise tile j holds dims 16 j + 4 lane group + r. osc: output factor
+// of dim class 2 (dim / 64) + (EVEN_ODD ? dim & 1 : 0).
+constexpr int FIN_ROW = D + 4;
 template <int NW>
 struct WaveVec;
 template <>
@@ -455,14 +472,22 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     v = sum_xor32(v);
     tot[k] = v;
   }
-  if (lc < 4) {
+  if (lc < 4) {  // lane (lane group, row lc) holds the row's sums for dims of its lane group
+    float* dst = acc_lds + (wv * 4 + lc) * FIN_ROW;
+    if constexpr (EVEN_ODD) {
+      // tiles 2 t and 2 t + 1: dims 32 t + 8 lq4 + 2 r + (0, 1)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int dim = EVEN_ODD ? 32 * (dt >> 1) + 2 * (4 * lq4 + r) + (dt & 1) : 16 * dt + 4 * lq4 + r;
-        acc_lds[(lc * D + dim) * NW + wv] = oacc[dt][r];
+      for (int t = 0; t < 4; ++t) {
+        const f4_t e = oacc[2 * t], o = oacc[2 * t + 1];
+        *reinterpret_cast<float4*>(dst + 32 * t + 8 * lq4) = make_float4(e[0], o[0], e[1], o[1]);
+        *reinterpret_cast<float4*>(dst + 32 * t + 8 * lq4 + 4) = make_float4(e[2], o[2], e[3], o[3]);
       }
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4*>(dst + 16 * dt + 4 * lq4) =
+            make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+    }
     if (lq4 == 0) {
       st_lds[(lc * 4 + 0) * NW + wv] = m_run;
       st_lds[(lc * 4 + 1) * NW + wv] = tot[0];
@@ -475,25 +500,31 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     }
   }
   __syncthreads();
-  for (int o = tid; o < R * D; o += 64 * NW) {
-    const int col = o / D;
-    const int d = o - col * D;
+  // two dims (d, d + 1) of row col per item
+  for (int o = tid; o < R * (D / 2); o += 64 * NW) {
+    const int col = o / (D / 2);
+    const int d = 2 * (o - col * (D / 2));
     const int g = d >> 6;
     const wvec m = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 0) * NW);
     const wvec bs = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 2 + g) * NW);
-    const wvec os = *reinterpret_cast<const wvec*>(st_lds + (16 + 2 * g + (EVEN_ODD ? d & 1 : 0)) * NW);
-    const wvec ac = *reinterpret_cast<const wvec*>(acc_lds + (col * D + d) * NW);
+    const wvec os0 = *reinterpret_cast<const wvec*>(st_lds + (16 + 2 * g) * NW);
+    const wvec os1 = *reinterpret_cast<const wvec*>(st_lds + (16 + 2 * g + (EVEN_ODD ? 1 : 0)) * NW);
+    float2 ac[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      ac[w] = *reinterpret_cast<const float2*>(acc_lds + (w * 4 + col) * FIN_ROW + d);
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
-    float a = 0.0f;
+    float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float mw = WaveVec<NW>::get(m, w);
       const float e = mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M);
-      a += e * fmaf(WaveVec<NW>::get(ac, w), WaveVec<NW>::get(os, w), WaveVec<NW>::get(bs, w));
+      a0 += e * fmaf(ac[w].x, WaveVec<NW>::get(os0, w), WaveVec<NW>::get(bs, w));
+      a1 += e * fmaf(ac[w].y, WaveVec<NW>::get(os1, w), WaveVec<NW>::get(bs, w));
     }
-    st_agent(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a);
+    st_agent2(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a0, a1);
   }
   if (tid < R) {
     const int col = tid;

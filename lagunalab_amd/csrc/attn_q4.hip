@@ -48,7 +48,7 @@ struct Q4Smem {
       Q4Terms terms[QW];
     } loop;
     struct {
-      alignas(16) float acc[QW][4][D];
+      alignas(16) float acc[QW][4][FIN_ROW];
       alignas(16) float st[QW][4][6];
       int last;
     } fin;

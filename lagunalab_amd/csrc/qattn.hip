@@ -57,7 +57,7 @@ struct PackSmem {
       PackBuf buf[NWAVE][2];
       PackTerms terms[NWAVE];
     } loop;
-    alignas(16) float acc[NWAVE][4][D];  // wave partials, final merge
+    alignas(16) float acc[NWAVE][4][FIN_ROW];  // wave partials, final merge
   };
   alignas(16) float st[NWAVE][4][6];
 };
