@@ -23,46 +23,54 @@ constexpr int64_t MAX_SPLITS = 32;    // kernels that merge their own splits (me
 constexpr int64_t MERGE_SPLITS = 64;  // kernels whose splits decode_merge_kernel merges
 
 // ----------------------------------------------------------------------------------------------
-// merge kernel: two partial rows per workgroup (one wave), four dims per thread
+// merge kernel: 64 dims of one partial row per workgroup (one wave); each group of four dims is
+// merged by four lanes 16 apart, each over a quarter of the splits
 // ----------------------------------------------------------------------------------------------
 
 // rows = partial rows per sequence (Hq * L). A sequence has at most MS <= MERGE_SPLITS splits
-// (make_plan), so every thread loads all of them -- (m, l) and the 16 bytes of acc of its four
-// dims -- in one round trip and merges them in registers (log-sum-exp against the largest m).
+// (make_plan). Lane l takes dims d0 = 64 (workgroup % 2) + 4 (l % 16) .. d0 + 3 of the splits
+// l / 16 + 4 k, k < MS / 4: it loads their (m, l) and the 16 bytes of acc in one round trip, the
+// four lanes of a dim group find the largest m with two lane swaps, weigh their splits against it
+// (log-sum-exp) and add up their sums with two more swaps. Four lanes per dim group put the same
+// partials in flight with a quarter of the loads per lane and four times the waves.
 template <int MS>
 __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restrict__ part_acc,
                                                            const float2* __restrict__ part_ml,
                                                            int rows, int total_rows,
                                                            DecodePlan plan,
                                                            uint16_t* __restrict__ out) {
-  const int grow = blockIdx.x * 2 + (threadIdx.x >> 5);  // (sequence, row) index
-  if (grow >= total_rows) return;
+  constexpr int PER = MS / 4;
+  const int grow = blockIdx.x >> 1;  // (sequence, row) index
+  if (grow >= total_rows) return;    // workgroup-uniform
+  const int lane = threadIdx.x;
+  const int qt = lane >> 4;
+  const int d0 = 64 * (blockIdx.x & 1) + 4 * (lane & 15);
   const int b = grow / rows;
   const int hq = grow - b * rows;
-  const int d0 = 4 * (threadIdx.x & 31);
   const int s0 = plan.split_begin[b];
   const int ns = min(plan.split_begin[b + 1] - s0, MS);
-  float m[MS], l[MS];
-  float4 a[MS];
-  // The (m, l) index is the same in 32 lanes; hidden from the compiler so that the loads stay
+  float m[PER], l[PER];
+  float4 a[PER];
+  // The (m, l) index is the same in 16 lanes; hidden from the compiler so that the loads stay
   // vector loads issued together (as scalar loads it waited for each one in turn).
   int base = s0;
   asm volatile("" : "+v"(base));
 #pragma unroll
-  for (int k = 0; k < MS; ++k) {
-    const int64_t r = (int64_t)(base + min(k, ns - 1)) * rows + hq;
-    const float2 ml = part_ml[r];  // k >= ns: split ns - 1 again, weighted 0 below
+  for (int k = 0; k < PER; ++k) {
+    const int64_t r = (int64_t)(base + min(qt + 4 * k, ns - 1)) * rows + hq;
+    const float2 ml = part_ml[r];  // past ns: split ns - 1 again, weighted 0 below
     m[k] = ml.x;
     l[k] = ml.y;
     a[k] = *reinterpret_cast<const float4*>(part_acc + r * D + d0);
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < MS; ++k) M = fmaxf(M, m[k]);
+  for (int k = 0; k < PER; ++k) M = fmaxf(M, qt + 4 * k < ns ? m[k] : -INFINITY);
+  M = max_xor32(max_xor16(M));
   float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f, den = 0.0f;
 #pragma unroll
-  for (int k = 0; k < MS; ++k) {
-    const bool use = k < ns && m[k] != -INFINITY;
+  for (int k = 0; k < PER; ++k) {
+    const bool use = qt + 4 * k < ns && m[k] != -INFINITY;
     const float w = use ? __builtin_amdgcn_exp2f(m[k] - M) : 0.0f;  // argument <= 0
     n0 = fmaf(w, a[k].x, n0);
     n1 = fmaf(w, a[k].y, n1);
@@ -70,10 +78,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
     n3 = fmaf(w, a[k].w, n3);
     den = fmaf(w, l[k], den);
   }
-  const float inv = 1.0f / den;
-  const uint32_t lo = (uint32_t)f32_to_bf16(n0 * inv) | ((uint32_t)f32_to_bf16(n1 * inv) << 16);
-  const uint32_t hi = (uint32_t)f32_to_bf16(n2 * inv) | ((uint32_t)f32_to_bf16(n3 * inv) << 16);
-  *reinterpret_cast<uint2*>(out + (int64_t)grow * D + d0) = make_uint2(lo, hi);
+  n0 = sum_xor32(sum_xor16(n0));
+  n1 = sum_xor32(sum_xor16(n1));
+  n2 = sum_xor32(sum_xor16(n2));
+  n3 = sum_xor32(sum_xor16(n3));
+  den = sum_xor32(sum_xor16(den));
+  if (qt == 0) {
+    const float inv = 1.0f / den;
+    const uint32_t lo = (uint32_t)f32_to_bf16(n0 * inv) | ((uint32_t)f32_to_bf16(n1 * inv) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(n2 * inv) | ((uint32_t)f32_to_bf16(n3 * inv) << 16);
+    *reinterpret_cast<uint2*>(out + (int64_t)grow * D + d0) = make_uint2(lo, hi);
+  }
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -174,9 +189,8 @@ void launch_merge(const float* part_acc, const float2* part_ml, int rows_per_seq
   for (int64_t b = 0; b < B; ++b)
     most = std::max(most, plan.split_begin[b + 1] - plan.split_begin[b]);
   const int total = (int)(B * rows_per_seq);
-  // one wave per workgroup: 0.3-0.4 us per verify or 48q/8kv decode step less than four rows per
-  // 128-thread workgroup
-  const dim3 grid((unsigned)((total + 1) / 2)), block(64);
+  // one wave per half row (64 dims)
+  const dim3 grid((unsigned)(2 * total)), block(64);
   if (most <= 32)
     decode_merge_kernel<32><<<grid, block, 0, st>>>(part_acc, part_ml, rows_per_seq, total, plan, out);
   else
