@@ -77,6 +77,8 @@ struct DenseSmem {
     f4_t acc[DW][NT * 8][64];  // wave partials in register layout (epilogue)
   };
   alignas(16) float st[DW][16 * NT][4];  // m, l, bias sum 0, bias sum 1
+  alignas(16) float wgt[16 * NT][DW];    // per row: each wave's log-sum-exp weight times 2^24
+  float bsw[16 * NT][2];                 // per row: the weighted bias sums of the two groups
   struct {                             // fused append: new row n - L + j, quantized
     uint8_t k[MAX_NEW][D];
     uint8_t v[MAX_NEW][D];
@@ -641,26 +643,57 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   }
   __syncthreads();
 
-  // ---- merge the waves (log-sum-exp) into the workgroup's partial, in the same layout: item
-  // (8 nt + dt, lane) holds dims 16 dt + 4 (lane / 16) + (0..3) of query row 16 nt + lane % 16
+  // ---- merge the waves (log-sum-exp) into the workgroup's partial. Per row first: the waves'
+  // weights against the row's largest m (times 2^24: codes entered as c 2^-24), the weighted bias
+  // sums and the row's (M, l); then per item (8 nt + dt, lane), dims 16 dt + 4 (lane / 16) +
+  // (0..3) of query row 16 nt + lane % 16: bias sum + the weighted sum of the waves' accumulators.
+  if (tid < R) {
+    const int col = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
+    float l = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) {
+      const float* st = sm.st[w][col];
+      const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
+      sm.wgt[col][w] = e * 16777216.0f;
+      l += e * st[1];
+      b0 = fmaf(e, st[2], b0);
+      b1 = fmaf(e, st[3], b1);
+    }
+    sm.bsw[col][0] = b0;
+    sm.bsw[col][1] = b1;
+    float2* pml = args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col;
+    if constexpr (MERGE) {
+      st_agent(reinterpret_cast<float*>(pml), M);
+      st_agent(reinterpret_cast<float*>(pml) + 1, l);
+    } else {
+      *pml = make_float2(M, l);
+    }
+  }
+  __syncthreads();
   for (int it = tid; it < NT * 8 * 64; it += 64 * DW) {
     const int reg = it >> 6, ln = it & 63;
     const int col = 16 * (reg >> 3) + (ln & 15);
     if (col >= R) continue;
     const int dt = reg & 7;
-    const int g = dt >> 2;
-    float M = -INFINITY;
+    float wg[DW];
 #pragma unroll
-    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    f4_t a = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < DW; w += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(&sm.wgt[col][w]);
+      wg[w] = q4.x;
+      wg[w + 1] = q4.y;
+      wg[w + 2] = q4.z;
+      wg[w + 3] = q4.w;
+    }
+    const float bias = sm.bsw[col][dt >> 2];
+    f4_t a = {bias, bias, bias, bias};
 #pragma unroll
     for (int w = 0; w < DW; ++w) {
-      const float* st = sm.st[w][col];
-      const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
       const f4_t v = sm.acc[w][reg][ln];
-      const float bias = st[2 + g];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] += e * fmaf(v[r], 16777216.0f, bias);
+      for (int r = 0; r < 4; ++r) a[r] = fmaf(wg[w], v[r], a[r]);
     }
     const int d0 = 16 * dt + 4 * (ln >> 4);
     float* pa = args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d0;
@@ -669,25 +702,6 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
       for (int r = 0; r < 4; ++r) st_agent(pa + r, a[r]);
     } else {
       *reinterpret_cast<f4_t*>(pa) = a;
-    }
-  }
-  if (tid < R) {
-    const int col = tid;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    float l = 0.0f;
-#pragma unroll
-    for (int w = 0; w < DW; ++w) {
-      const float* st = sm.st[w][col];
-      l += st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M) * st[1];
-    }
-    float2* pml = args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col;
-    if constexpr (MERGE) {
-      st_agent(reinterpret_cast<float*>(pml), M);
-      st_agent(reinterpret_cast<float*>(pml) + 1, l);
-    } else {
-      *pml = make_float2(M, l);
     }
   }
   if constexpr (MERGE) {
