@@ -180,10 +180,13 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
     if (__builtin_amdgcn_ballot_w64(bump)) {
       const float mn = bump ? tmax : m_run;
       const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
-      m_run = mn;
-      lsum *= alpha;
+      // while no lane has seen a key (the wave's first super-tile) the sums are all zero
+      if (__builtin_amdgcn_ballot_w64(m_run != -INFINITY)) {
+        lsum *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+      }
+      m_run = mn;
     }
     const float mref = m_run == -INFINITY ? 0.0f : m_run;
     uint32_t ph[4], pl[4];

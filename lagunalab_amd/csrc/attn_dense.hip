@@ -378,12 +378,15 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
         if (bumps) {
           const float mn = bump ? tmax : m_run[nt];
           const float alpha = m_run[nt] == -INFINITY ? 0.0f : exp2_nonpos(m_run[nt] - mn);
-          m_run[nt] = mn;
-          lsum[nt] *= alpha;
-          bsum[nt][0] *= alpha;
-          bsum[nt][1] *= alpha;
+          // while no lane has seen a key of these rows the sums are all zero
+          if (__builtin_amdgcn_ballot_w64(m_run[nt] != -INFINITY)) {
+            lsum[nt] *= alpha;
+            bsum[nt][0] *= alpha;
+            bsum[nt][1] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+            for (int dt = 0; dt < 8; ++dt) oacc[nt][dt] *= alpha;
+          }
+          m_run[nt] = mn;
         }
         if (vn) {  // every N tile's accumulators; the V terms read below are rewritten
           vscale_apply<NT>(va0, va1, vsc, &oacc[0][0]);

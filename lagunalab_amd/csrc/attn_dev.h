@@ -131,13 +131,16 @@ __device__ __forceinline__ void vscale_apply(float a0, float a1, VScale& v, f4_t
   const float m0 = wave_max_valu(a0), m1 = wave_max_valu(a1);
   const int n0 = m0 > 0.0f ? pow2_exp_into(m0, 5, -40, 40) : v.k0;
   const int n1 = m1 > 0.0f ? pow2_exp_into(m1, 5, -40, 40) : v.k1;
-  // exact power-of-two ratios; an unset factor (0) had produced zero accumulators
+  // exact power-of-two ratios; an unset factor (0) had produced zero accumulators, so with both
+  // unset (the first super-tile) nothing is scaled (wave-uniform)
   const float r0 = v.k0 == VK_NONE ? 0.0f : pow2f(n0 - v.k0);
   const float r1 = v.k1 == VK_NONE ? 0.0f : pow2f(n1 - v.k1);
+  if (v.k0 != VK_NONE || v.k1 != VK_NONE) {
 #pragma unroll
-  for (int i = 0; i < NACC; ++i)
+    for (int i = 0; i < NACC; ++i)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) oacc[8 * i + dt] *= dt < 4 ? r0 : r1;
+      for (int dt = 0; dt < 8; ++dt) oacc[8 * i + dt] *= dt < 4 ? r0 : r1;
+  }
   v.k0 = n0;
   v.k1 = n1;
   v.f0 = n0 == VK_NONE ? 0.0f : pow2f(n0);

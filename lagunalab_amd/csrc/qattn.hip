@@ -287,12 +287,15 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
       if (bumps) {
         const float mn = bump ? tmax : m_run;
         const float alpha = m_run == -INFINITY ? 0.0f : exp2_nonpos(m_run - mn);
-        m_run = mn;
-        lsum *= alpha;
-        bsum0 *= alpha;
-        bsum1 *= alpha;
+        // while no lane has seen a key (the wave's first super-tile) the sums are all zero
+        if (__builtin_amdgcn_ballot_w64(m_run != -INFINITY)) {
+          lsum *= alpha;
+          bsum0 *= alpha;
+          bsum1 *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+          for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+        }
+        m_run = mn;
       }
       if (vnew) {  // the terms read below are rewritten with the new factors
         vscale_apply(va0, va1, vsc, oacc);
