@@ -226,9 +226,26 @@ __device__ __forceinline__ float rope_partner(float y, int lane, int off, int pa
   return __shfl(y, partner, 64);
 }
 
-__device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,
-                                                   const float* __restrict__ inv_freq,
-                                                   int rot_dims, float mscale, float pos) {
+// The rotation of lane `lane` at position pos: sin and cos of its two angles (the same for every
+// row at that position), whether its dims rotate and whether they are the first half's.
+struct RopeLane {
+  float s0, c0, s1, c1;
+  bool rot, first;
+};
+__device__ __forceinline__ RopeLane rope_lane(int lane, const float* __restrict__ inv_freq,
+                                              int rot_dims, float pos) {
+  RopeLane r{0.f, 1.f, 0.f, 1.f, 2 * lane < rot_dims, 4 * lane < rot_dims};
+  if (r.rot) {
+    const int i0 = r.first ? 2 * lane : 2 * lane - (rot_dims >> 1);
+    sincos_reduced(pos * inv_freq[i0], &r.s0, &r.c0);
+    sincos_reduced(pos * inv_freq[i0 + 1], &r.s1, &r.c1);
+  }
+  return r;
+}
+
+// RMSNorm of a row held two values per lane, then the rotation rl (from rope_lane).
+__device__ __forceinline__ uint32_t norm_rope_apply(uint32_t x2, uint32_t w2, int lane, float eps,
+                                                    const RopeLane& rl, int rot_dims, float mscale) {
   const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
   float ss = x0 * x0 + x1 * x1;  // sum over the wave: rows of 16 by DPP, then row swaps
   ss += dpp<DPP_QUAD_XOR1>(ss);
@@ -243,26 +260,27 @@ __device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int
 
   const int half = rot_dims >> 1;      // rotated pairs
   const int lane_off = rot_dims >> 2;  // partner lane distance
-  const bool rot = 2 * lane < rot_dims;
-  const int partner = rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
+  const int partner = rl.rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
   const float p0 = rope_partner(y0, lane, lane_off, partner);
   const float p1 = rope_partner(y1, lane, lane_off, partner);
-  if (rot) {
-    const bool first = 2 * lane < half;  // dims i < half: out = x_i cos - x_{i+half} sin
-    const int i0 = first ? 2 * lane : 2 * lane - half;
-    float s0, c0, s1, c1;
-    sincos_reduced(pos * inv_freq[i0], &s0, &c0);
-    sincos_reduced(pos * inv_freq[i0 + 1], &s1, &c1);
+  if (rl.rot) {
     const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
-    if (first) {
-      y0 = a0 * c0 - b0 * s0;
-      y1 = a1 * c1 - b1 * s1;
+    if (rl.first) {  // dims i < half: out = x_i cos - x_{i+half} sin
+      y0 = a0 * rl.c0 - b0 * rl.s0;
+      y1 = a1 * rl.c1 - b1 * rl.s1;
     } else {  // this lane holds x_{i+half}; the partner holds x_i
-      y0 = b0 * s0 + a0 * c0;
-      y1 = b1 * s1 + a1 * c1;
+      y0 = b0 * rl.s0 + a0 * rl.c0;
+      y1 = b1 * rl.s1 + a1 * rl.c1;
     }
   }
   return (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+}
+
+__device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,
+                                                   const float* __restrict__ inv_freq,
+                                                   int rot_dims, float mscale, float pos) {
+  return norm_rope_apply(x2, w2, lane, eps, rope_lane(lane, inv_freq, rot_dims, pos), rot_dims,
+                         mscale);
 }
 
 }  // namespace lq

@@ -416,23 +416,21 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   else
     asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
   if constexpr (NORM) {
-    // Raw q rows and new K row -> RMSNorm + RoPE at position n - 1. Row j (q rows 0 .. R - 1, the
-    // K row as j = R) is done by wave j % NWAVE from its own staged copy and written into every
-    // wave's copy; the barriers order the copies' landing and the writes.
-    __syncthreads();  // every wave's staged rows have landed (each waited for its own above)
-    const uint8_t* own = reinterpret_cast<const uint8_t*>(&tm);
-    const float pos = (float)(n - 1);
-    for (int j = wv; j <= R; j += NWAVE) {  // wave-uniform
-      const int off = j < R ? j * 2 * D : 1024;
-      const uint32_t w2 = reinterpret_cast<const uint32_t*>(own + (j < R ? 1536 : 1792))[lane];
-      const uint32_t y = norm_rope_lane(reinterpret_cast<const uint32_t*>(own + off)[lane], w2,
-                                        lane, nargs.norm_eps, &nsm.inv_freq[wv][0], nargs.rot_dims,
-                                        nargs.mscale, pos);
-#pragma unroll
-      for (int w = 0; w < NWAVE; ++w)
-        reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(&sm.loop.terms[w]) + off)[lane] = y;
+    // Raw q rows and new K row -> RMSNorm + RoPE at position n - 1, in place: every wave
+    // normalizes and rotates its own staged copies (rows 0 .. R - 1 q, then the K row), with the
+    // rotation's sin and cos computed once for all rows; no wave touches another's copies.
+    uint8_t* own = reinterpret_cast<uint8_t*>(&tm);
+    const RopeLane rl = rope_lane(lane, &nsm.inv_freq[wv][0], nargs.rot_dims, (float)(n - 1));
+    const uint32_t wq = reinterpret_cast<const uint32_t*>(own + 1536)[lane];
+    const uint32_t wk = reinterpret_cast<const uint32_t*>(own + 1792)[lane];
+    for (int j = 0; j <= R; ++j) {  // wave-uniform
+      uint32_t* row = reinterpret_cast<uint32_t*>(own + (j < R ? j * 2 * D : 1024));
+      row[lane] = norm_rope_apply(row[lane], j < R ? wq : wk, lane, nargs.norm_eps, rl,
+                                  nargs.rot_dims, nargs.mscale);
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the rows are read whole below
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt, times
