@@ -266,6 +266,27 @@ def test_ragged_matches_per_sequence_oracle(dev):
     assert_attn_close(got, want, "ragged unfused", REF_SMALL_N_ATOL, 0.0)
 
 
+@pytest.mark.parametrize("G", [6, 8, 16])
+def test_ragged_dense_kernel_matches_per_sequence_oracle(dev, G):
+    """Batches with more than 4 query rows per KV head run the dense kernel: with 6 or 8 rows
+    (48q/8kv, 64q/8kv) it merges each sequence's splits in its last workgroup, with 16 rows the
+    split merge is a launch of its own. The lengths give sequences of one split up to sixteen
+    (at least 256 keys per split), so that the per-sequence merge sees fewer splits than the
+    merge's four lanes per dim group as well as many."""
+    from lagunalab_amd.q8_attn import decode_attention
+    rng = np.random.default_rng(60 + G)
+    lens = [130, 1, 4097, 700, 255, 2049]
+    B, cap = len(lens), 4352
+    kq, vq = make_cache(rng, B, 8, cap, cap, dev)
+    q = Q.randn_bf16(rng, (B, 8 * G, 1, 128))
+    got = decode_attention(to_dev_bf16(q, dev), kq, vq, lens=lens, scale=128 ** -0.5)
+    kn, vn = cache_np(kq), cache_np(vq)
+    want = A.ragged_unfused_attention(q, kn, vn, lens, 128 ** -0.5, fused=True)
+    assert_attn_close(got, want, f"ragged dense G={G} fused")
+    want = A.ragged_unfused_attention(q, kn, vn, lens, 128 ** -0.5)
+    assert_attn_close(got, want, f"ragged dense G={G} unfused", REF_SMALL_N_ATOL, 0.0)
+
+
 def test_ragged_session_lengths_match_single_calls(dev):
     """Config 3's lengths (default_rng(1) in [42771, 82671]): the variable-length call equals one
     call per sequence (size-independent property; per-sequence calls are checked above)."""
