@@ -692,6 +692,30 @@ def test_verify_matches_causal_oracle(dev, n, L, G):
                       f"unfused verify n={n} L={L} G={G}", at, rt)
 
 
+@pytest.mark.parametrize("kind,L,G", [("verify", 5, 4), ("decode", 1, 6), ("decode", 1, 16)])
+def test_two_kv_heads_many_splits_match_oracle(dev, kind, L, G):
+    """Two KV heads give each head 128 workgroups' worth of splits: the dense kernel's merge launch
+    then takes up to 64 splits per sequence (verify, and decode with 16 rows per KV head: the
+    merge with 16 splits per lane), while the in-kernel merge (decode with 6 rows) caps them at 32."""
+    from lagunalab_amd.q8_attn import decode_attention, q8_verify_attention
+    rng = np.random.default_rng(90 + G * L)
+    Hkv, n = 2, 20000
+    cap = (n + 255) // 256 * 256
+    kq, vq = make_cache(rng, 1, Hkv, n, cap, dev)
+    q = Q.randn_bf16(rng, (1, Hkv * G, L, 128))
+    scale = 128 ** -0.5
+    if kind == "verify":
+        got = q8_verify_attention(to_dev_bf16(q, dev), kq, vq, n, scale)
+    else:
+        got = decode_attention(to_dev_bf16(q, dev), kq, vq, n=n, scale=scale)
+    kn, vn = cache_np(kq), cache_np(vq)
+    causal = kind == "verify"
+    assert_attn_close(got, A.fused_attention(q, kn, vn, n, scale, causal=causal),
+                      f"{kind} Hkv=2 G={G} L={L} fused")
+    assert_attn_close(got, A.unfused_attention(q, kn, vn, n, scale, causal=causal),
+                      f"{kind} Hkv=2 G={G} L={L} unfused")
+
+
 @pytest.mark.parametrize("n,L,G", [(1500, 4, 1), (900, 2, 2), (130, 3, 1), (70000, 2, 2)])
 def test_verify_packed_kernel_matches_causal_oracle(dev, n, L, G):
     """G * L <= 4 rows per KV head over two sequences, or one of more than 65,536 rows: the
