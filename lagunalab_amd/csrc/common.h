@@ -186,14 +186,14 @@ __device__ __forceinline__ float wave_min(float x) {
   return x;
 }
 
+// Sum over all 64 lanes, in every lane, on the VALU (DPP row steps, then the row and half
+// swaps): no LDS round trips, unlike a butterfly of cross-lane reads. All lanes active.
 __device__ __forceinline__ float wave_sum(float x) {
   x += dpp<DPP_QUAD_XOR1>(x);
   x += dpp<DPP_QUAD_XOR2>(x);
   x += dpp<DPP_ROW_ROR4>(x);
   x += dpp<DPP_ROW_ROR8>(x);
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  return sum_xor32(sum_xor16(x));
 }
 
 // RMSNorm (times w, rounded to bf16) and RoPE at position `pos` of one 128-dim head row held by

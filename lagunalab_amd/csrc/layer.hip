@@ -178,9 +178,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint16_t* __restri
   }
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    float a = acc[r];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
+    const float a = wave_sum(acc[r]);
     if (lane == r && r0 + r < N) y[r0 + r] = f32_to_bf16(a);
   }
 }
@@ -295,8 +293,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
         s += bf16_lo(xw[j]) * bf16_lo(xw[j]) + bf16_hi(xw[j]) * bf16_hi(xw[j]);
       ss += tid + 256 * i < chunks ? s : 0.0f;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = wave_sum(ss);
     if (lane == 0) red[tid >> 6] = ss;
     __syncthreads();
     inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
@@ -349,10 +346,7 @@ __global__ __launch_bounds__(256) void gemv_fused_kernel(const uint16_t* W, cons
     uint16_t o[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      float a = acc[r];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
-      o[r] = f32_to_bf16(a);
+      o[r] = f32_to_bf16(wave_sum(acc[r]));
     }
     if (head_rows) {  // rows r0, r0 + 1 of one q/k head (r0 even): one agent-scope word
       if (lane == 0)
