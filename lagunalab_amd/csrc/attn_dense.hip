@@ -526,9 +526,7 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
           mbits = bf16x2_absmax_bits(mbits, qwd[nt][g][j]);
           s += bf16_lo(qwd[nt][g][j]) + bf16_hi(qwd[nt][g][j]);
         }
-        s += shfl_xor_f(s, 16);
-        s += shfl_xor_f(s, 32);
-        qsum[nt][g] = s * qk_scale_log2;
+        qsum[nt][g] = sum_xor32(sum_xor16(s)) * qk_scale_log2;
       }
     }
     const int kq = q_pow2_exp(bf16x2_max_value(mbits));

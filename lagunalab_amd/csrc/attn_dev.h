@@ -44,7 +44,6 @@ __device__ __forceinline__ uint32_t pack_h2(float x, float y) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-__device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
 
 // One bf16 half of a word as fp32 with one v_perm_b32, the half chosen by a per-lane selector
 // (SEL_LO: bits 0-15, SEL_HI: bits 16-31, moved to the top, zeros below).
