@@ -66,6 +66,7 @@ struct DenseTerms {  // per key of the current super-tile
 };
 
 constexpr int MAX_NEW = 16;  // rows of a fused append (verify L <= 16)
+typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
 
 template <int NT, int ST, int DW>
 struct DenseSmem {
@@ -631,78 +632,111 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
     bsum[nt][0] = sum_xor32(sum_xor16(bsum[nt][0]));
     bsum[nt][1] = sum_xor32(sum_xor16(bsum[nt][1]));
   }
-  __syncthreads();  // every wave is done with its LDS tiles before they are reused below
   // Wave partials go to LDS as the registers hold them (lane-contiguous 16-byte writes, no bank
-  // conflicts): acc[w][8 nt + dt][lane] = oacc[nt][dt] of wave w.
+  // conflicts), each wave into its own two tile buffers, which are free once its loop has ended
+  // (its copies have all landed: vmcnt 0 above), so no barrier comes first and the waves that
+  // end early write while the others finish: accw(w)[8 nt + dt][lane] = oacc[nt][dt] of wave w.
+  static_assert(sizeof(sm.loop.buf[0]) >= sizeof(f4_t) * NT * 8 * 64, "wave partial too large");
+  auto accw = [&](int w) { return reinterpret_cast<f4_t(*)[64]>(&sm.loop.buf[w][0]); };
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) sm.acc[wv][8 * nt + dt][lane] = oacc[nt][dt];
+    for (int dt = 0; dt < 8; ++dt) accw(wv)[8 * nt + dt][lane] = oacc[nt][dt];
     if (lq4 == 0)
       *reinterpret_cast<float4*>(sm.st[wv][nt * 16 + lc]) =
           make_float4(m_run[nt], lsum[nt], bsum[nt][0], bsum[nt][1]);
   }
   __syncthreads();
 
-  // ---- merge the waves (log-sum-exp) into the workgroup's partial. Per row first: the waves'
-  // weights against the row's largest m (times 2^24: codes entered as c 2^-24), the weighted bias
-  // sums and the row's (M, l); then per item (8 nt + dt, lane), dims 16 dt + 4 (lane / 16) +
-  // (0..3) of query row 16 nt + lane % 16: bias sum + the weighted sum of the waves' accumulators.
-  if (tid < R) {
-    const int col = tid;
-    float M = -INFINITY;
+  // ---- merge the waves (log-sum-exp) into the workgroup's partial: per row the waves' weights
+  // against the row's largest m (times 2^24: codes entered as c 2^-24), the weighted bias sums
+  // and the row's (M, l); per item (8 nt + dt, lane), dims 16 dt + 4 (lane / 16) + (0..3) of
+  // query row 16 nt + lane % 16: bias sum + the weighted sum of the waves' accumulators.
+  if constexpr (MERGE) {
+    // One item per thread (one N tile on 8 waves: dt = wave), which computes its row's weights
+    // itself (DW exp2), so that no second barrier and no serial per-row step come before the
+    // sums; agent-scope partial stores, 16 bytes per item.
+    const int col = lane & 15;
+    if (col < R) {
+      float4 stw[DW];
+      float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
-    float l = 0.0f, b0 = 0.0f, b1 = 0.0f;
+      for (int w = 0; w < DW; ++w) {
+        stw[w] = *reinterpret_cast<const float4*>(sm.st[w][col]);
+        M = fmaxf(M, stw[w].x);
+      }
+      float ew[DW], bias = 0.0f;
 #pragma unroll
-    for (int w = 0; w < DW; ++w) {
-      const float* st = sm.st[w][col];
-      const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
-      sm.wgt[col][w] = e * 16777216.0f;
-      l += e * st[1];
-      b0 = fmaf(e, st[2], b0);
-      b1 = fmaf(e, st[3], b1);
+      for (int w = 0; w < DW; ++w) {
+        ew[w] = stw[w].x == -INFINITY ? 0.0f : exp2_nonpos(stw[w].x - M);
+        bias = fmaf(ew[w], wv < 4 ? stw[w].z : stw[w].w, bias);
+      }
+      f4_t a = {bias, bias, bias, bias};
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const f4_t v = accw(w)[wv][lane];
+        const float wg = ew[w] * 16777216.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = fmaf(wg, v[r], a[r]);
+      }
+      const int64_t prow = (int64_t)x * Hkv * R + (int64_t)hk * R + col;
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc(args.part_acc, 0, 0x7fffffff, 0x00020000);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(v4u32_t, a), rsrc,
+          (int)((prow * D + 16 * wv + 4 * lq4) * (int64_t)sizeof(float)), 0, 16);  // sc1
+      if (tid < R) {  // wave 0, lane = row
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DW; ++w) l += ew[w] * stw[w].y;
+        st_agent2(reinterpret_cast<float*>(args.part_ml + prow), M, l);
+      }
     }
-    sm.bsw[col][0] = b0;
-    sm.bsw[col][1] = b1;
-    float2* pml = args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col;
-    if constexpr (MERGE) {
-      st_agent(reinterpret_cast<float*>(pml), M);
-      st_agent(reinterpret_cast<float*>(pml) + 1, l);
-    } else {
-      *pml = make_float2(M, l);
+  } else {
+    if (tid < R) {
+      const int col = tid;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
+      float l = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const float* st = sm.st[w][col];
+        const float e = st[0] == -INFINITY ? 0.0f : exp2_nonpos(st[0] - M);
+        sm.wgt[col][w] = e * 16777216.0f;
+        l += e * st[1];
+        b0 = fmaf(e, st[2], b0);
+        b1 = fmaf(e, st[3], b1);
+      }
+      sm.bsw[col][0] = b0;
+      sm.bsw[col][1] = b1;
+      args.part_ml[(int64_t)x * Hkv * R + (int64_t)hk * R + col] = make_float2(M, l);
     }
-  }
-  __syncthreads();
-  for (int it = tid; it < NT * 8 * 64; it += 64 * DW) {
-    const int reg = it >> 6, ln = it & 63;
-    const int col = 16 * (reg >> 3) + (ln & 15);
-    if (col >= R) continue;
-    const int dt = reg & 7;
-    float wg[DW];
+    __syncthreads();
+    for (int it = tid; it < NT * 8 * 64; it += 64 * DW) {
+      const int reg = it >> 6, ln = it & 63;
+      const int col = 16 * (reg >> 3) + (ln & 15);
+      if (col >= R) continue;
+      const int dt = reg & 7;
+      float wg[DW];
 #pragma unroll
-    for (int w = 0; w < DW; w += 4) {
-      const float4 q4 = *reinterpret_cast<const float4*>(&sm.wgt[col][w]);
-      wg[w] = q4.x;
-      wg[w + 1] = q4.y;
-      wg[w + 2] = q4.z;
-      wg[w + 3] = q4.w;
-    }
-    const float bias = sm.bsw[col][dt >> 2];
-    f4_t a = {bias, bias, bias, bias};
+      for (int w = 0; w < DW; w += 4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&sm.wgt[col][w]);
+        wg[w] = q4.x;
+        wg[w + 1] = q4.y;
+        wg[w + 2] = q4.z;
+        wg[w + 3] = q4.w;
+      }
+      const float bias = sm.bsw[col][dt >> 2];
+      f4_t a = {bias, bias, bias, bias};
 #pragma unroll
-    for (int w = 0; w < DW; ++w) {
-      const f4_t v = sm.acc[w][reg][ln];
+      for (int w = 0; w < DW; ++w) {
+        const f4_t v = accw(w)[reg][ln];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a[r] = fmaf(wg[w], v[r], a[r]);
-    }
-    const int d0 = 16 * dt + 4 * (ln >> 4);
-    float* pa = args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d0;
-    if constexpr (MERGE) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) st_agent(pa + r, a[r]);
-    } else {
-      *reinterpret_cast<f4_t*>(pa) = a;
+        for (int r = 0; r < 4; ++r) a[r] = fmaf(wg[w], v[r], a[r]);
+      }
+      const int d0 = 16 * dt + 4 * (ln >> 4);
+      *reinterpret_cast<f4_t*>(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d0) = a;
     }
   }
   if constexpr (MERGE) {
