@@ -32,10 +32,7 @@ struct Bf16Buf {
 };
 
 struct Bf16Smem {
-  union {
-    Bf16Buf buf[BW][2];
-    alignas(16) float acc[BW][4][FIN_ROW];
-  };
+  Bf16Buf buf[BW][2];  // a wave's two also hold its partial rows after its loop
   alignas(16) float st[BW][4][6];
   alignas(16) uint8_t qstage[BW][4 * D * 2];  // each wave's copy of the (<= 4) q rows
 };
@@ -266,10 +263,11 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
     process(si + 1, B1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();  // every wave is done with its LDS tiles before they are reused below
   const float osc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  packed_finish<BW>(oacc, m_run, lsum, 0.0f, 0.0f, osc, &sm.acc[0][0][0], &sm.st[0][0][0],
-                    &sh_last, args, plan, x, b, hk, R);
+  static_assert(sizeof(sm.buf[0]) >= sizeof(float) * 6 * 128, "wave buffers hold the finish rows");
+  packed_finish<BW>(oacc, m_run, lsum, 0.0f, 0.0f, osc, reinterpret_cast<float*>(&sm.buf[0][0]),
+                    (int)(sizeof(sm.buf[0]) / sizeof(float)), &sm.st[0][0][0], &sh_last, args,
+                    plan, x, b, hk, R);
 }
 
 }  // namespace

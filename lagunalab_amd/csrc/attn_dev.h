@@ -411,14 +411,17 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 // query row are summed (lanes 4 and 8 apart in a row), the softmax sum and the two bias sums over
 // all lanes; then the NW waves meet in LDS and their log-sum-exp merge is the workgroup's split
 // partial: acc * (the wave's output factor of the dim's class, osc) + bias sum of the quant
-// group, written with agent-scope stores. LDS layout: acc_lds [NW][4 rows][FIN_ROW] (a wave's row
-// of D floats, padded by 16 bytes so that the four rows' 16-byte writes of one instruction fall in
-// different banks: each lane holding a row writes its dims with 8 ds_write_b128), st_lds
-// [4][4][NW]: m, l, bias sum 0, bias sum 1 of each wave side by side, then [4][NW]: the output
-// factors. Each output pair of dims then takes NW 8-byte reads and three NW-wide reads. Then the
-// arrival count, and the last workgroup of the (sequence, KV head) merges all splits
-// (merge_rows4). The caller has synchronised the workgroup so that acc_lds/st_lds (16-byte
-// aligned, at least 4 FIN_ROW NW and 20 NW floats) may overwrite its tile buffers.
+// group, written with agent-scope stores. LDS layout: wave w's 4 rows at acc_lds + w acc_ws, rows
+// FIN_ROW floats apart (a row of D floats, padded by 16 bytes so that the four rows' 16-byte
+// writes of one instruction fall in different banks: each lane holding a row writes its dims with
+// 8 ds_write_b128) -- in the wave's own tile buffers, free once its loop has ended, so the caller
+// needs no barrier before this and waves that end early write while the others finish; st_lds
+// [4][4][NW] (outside every wave's buffers): m, l, bias sum 0, bias sum 1 of each wave side by
+// side, then [4][NW]: the output factors. Each output pair of dims then takes NW 8-byte reads and
+// three NW-wide reads. Then the arrival count, and the last workgroup of the (sequence, KV head)
+// merges all splits (merge_rows4, with acc_lds as its scratch). acc_lds and st_lds 16-byte
+// aligned; each wave's area at least 4 FIN_ROW floats, wave 0's at least 6 * 128 (merge
+// scratch), st_lds 20 NW floats.
 // EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (4 lane group + r) + p (the 4-bit
 // kernel's P.V operands); otherwise tile j holds dims 16 j + 4 lane group + r. osc: output factor
 // of dim class 2 (dim / 64) + (EVEN_ODD ? dim & 1 : 0).
@@ -440,9 +443,9 @@ struct WaveVec<2> {
 
 template <int NW, bool EVEN_ODD = false>
 __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bsum0, float bsum1,
-                              const float (&osc)[4], float* acc_lds, float* st_lds, int* sh_last,
-                              const AttnArgs& args, const DecodePlan& plan, int x, int b, int hk,
-                              int R) {
+                              const float (&osc)[4], float* acc_lds, int acc_ws, float* st_lds,
+                              int* sh_last, const AttnArgs& args, const DecodePlan& plan, int x,
+                              int b, int hk, int R) {
   typedef typename WaveVec<NW>::T wvec;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -475,7 +478,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     tot[k] = v;
   }
   if (lc < 4) {  // lane (lane group, row lc) holds the row's sums for dims of its lane group
-    float* dst = acc_lds + (wv * 4 + lc) * FIN_ROW;
+    float* dst = acc_lds + wv * acc_ws + lc * FIN_ROW;
     if constexpr (EVEN_ODD) {
       // tiles 2 t and 2 t + 1: dims 32 t + 8 lq4 + 2 r + (0, 1)
 #pragma unroll
@@ -514,7 +517,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     float2 ac[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w)
-      ac[w] = *reinterpret_cast<const float2*>(acc_lds + (w * 4 + col) * FIN_ROW + d);
+      ac[w] = *reinterpret_cast<const float2*>(acc_lds + w * acc_ws + col * FIN_ROW + d);
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));

@@ -44,18 +44,16 @@ struct Q4Terms {  // per key of the current super-tile
 };
 
 struct Q4Smem {
-  union {
-    struct {
-      Q4Buf buf[QW][2];
-      Q4Terms terms[QW];
-    } loop;
-    struct {
-      alignas(16) float acc[QW][4][FIN_ROW];
-      alignas(16) float st[QW][4][6];
-      int last;
-    } fin;
-  };
+  struct {
+    Q4Buf buf[QW][2];  // a wave's two also hold its partial rows after its loop
+    Q4Terms terms[QW];
+  } loop;
+  struct {
+    alignas(16) float st[QW][4][6];
+    int last;
+  } fin;
 };
+static_assert(sizeof(Q4Buf) * 2 >= sizeof(float) * 6 * 128, "wave buffers hold the finish rows");
 
 // 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals, in the
 // k-slot order {0, 4, 1, 5, 2, 6, 3, 7}: masks keep two nibbles per word, one in each half, so
@@ -398,9 +396,10 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   float osc[4];  // output factors: 2^24 over the P.V factors, and 1/16 for the odd dims (their
   vscale_out(vsc, 16777216.0f, 0.0625f, osc);  // codes entered as 16 c)
-  __syncthreads();
-  packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, osc, &sm.fin.acc[0][0][0],
-                          &sm.fin.st[0][0][0], &sm.fin.last, args, plan, x, b, hk, R);
+  packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, osc,
+                          reinterpret_cast<float*>(&sm.loop.buf[0][0]),
+                          (int)(sizeof(sm.loop.buf[0]) / sizeof(float)), &sm.fin.st[0][0][0],
+                          &sm.fin.last, args, plan, x, b, hk, R);
 }
 
 }  // namespace

@@ -52,15 +52,13 @@ struct PackTerms {  // per key of the current super-tile
 };
 
 struct PackSmem {
-  union {
-    struct {
-      PackBuf buf[NWAVE][2];
-      PackTerms terms[NWAVE];
-    } loop;
-    alignas(16) float acc[NWAVE][4][FIN_ROW];  // wave partials, final merge
-  };
+  struct {
+    PackBuf buf[NWAVE][2];  // a wave's two also hold its partial rows after its loop
+    PackTerms terms[NWAVE];
+  } loop;
   alignas(16) float st[NWAVE][4][6];
 };
+static_assert(sizeof(PackBuf) * 2 >= sizeof(float) * 6 * 128, "wave buffers hold the finish rows");
 
 // The NORM variant's extra staging (RoPE frequencies of each wave's copy).
 template <bool NORM>
@@ -546,9 +544,10 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
 
   float osc[4];  // output factors: 2^24 (codes entered as c 2^-24) over the P.V factors
   vscale_out(vsc, 16777216.0f, 1.0f, osc);
-  __syncthreads();  // every wave is done with its LDS tiles before they are reused below
-  packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, osc, &sm.acc[0][0][0],
-                       &sm.st[0][0][0], &sh_last, args, plan, x, b, hk, R);
+  packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, osc,
+                       reinterpret_cast<float*>(&sm.loop.buf[0][0]),
+                       (int)(sizeof(sm.loop.buf[0]) / sizeof(float)), &sm.st[0][0][0], &sh_last,
+                       args, plan, x, b, hk, R);
 }
 
 template <bool CAUSAL>
