@@ -51,16 +51,18 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
   const float qk_scale_log2 = args.qk_scale_log2;
+  LQ_ARG_BATCH("s"(q), "s"(kc), "s"(vc), "s"(cap), "s"(Hkv), "s"(G), "s"(L), "s"(plan.nseq),
+               "s"(plan.chunk), "s"(plan.split_begin[1]), "s"(plan.len[0]));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int x = blockIdx.x;
   const int hk = blockIdx.y;
-  int b;
-  find_seq(plan, x, b);
-  const int n = plan.len[b];
-  const int c_begin = (x - plan.split_begin[b]) * plan.chunk;
+  const SeqSplits sq = seq_splits(plan, x);
+  const int b = sq.b;
+  const int n = sq.len;
+  const int c_begin = (x - sq.s0) * plan.chunk;
   const int c_end = min(c_begin + plan.chunk, n);
   const int sub = (c_end - c_begin + BW - 1) / BW;
   const int w_begin = min(c_begin + wv * sub, c_end);

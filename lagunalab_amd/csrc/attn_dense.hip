@@ -113,20 +113,23 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
   const float qk_scale_log2 = args.qk_scale_log2;
+  LQ_ARG_BATCH("s"(q), "s"(args.kc), "s"(args.vc), "s"(args.ks), "s"(args.kb), "s"(args.vs),
+               "s"(args.vb), "s"(args.knew), "s"(args.vnew), "s"(args.pos), "s"(cap), "s"(Hkv),
+               "s"(G), "s"(L), "s"(plan.nseq), "s"(plan.split_begin[1]), "s"(plan.len[0]));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
   const int x = blockIdx.x;
   const int hk = blockIdx.y;
-  int b;
-  find_seq(plan, x, b);
+  const SeqSplits sq = seq_splits(plan, x);
+  const int b = sq.b;
   // rows after the append: the host's length, or (decode from device positions) pos[b] + 1
   const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap)
-                         : plan.len[b];
+                         : sq.len;
   const int T = (n + DST - 1) / DST;
-  const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * DW;
-  const int gw = (x - plan.split_begin[b]) * DW + wv;
+  const int NWS = sq.ns * DW;
+  const int gw = (x - sq.s0) * DW + wv;
   const int R = G * L;  // query rows of this KV head, <= 16 NT
   const int Hq = Hkv * G;
   const int64_t row0 = ((int64_t)b * Hkv + hk) * cap;
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   const bool app = args.knew != nullptr;
   const int na = n - L;
   const int ta = na / DST, tb = (n - 1) / DST;
-  const int xs = x - plan.split_begin[b];
+  const int xs = x - sq.s0;
   const bool wg_a = app && (ta % NWS) / DW == xs;
   const bool wg_b = app && tb != ta && (tb % NWS) / DW == xs;
   const int sr0 = wg_a ? na : tb * DST;  // rows staged by this workgroup: [sr0, sr1)
@@ -747,7 +750,7 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
     __syncthreads();
     if (tid == 0) {
       uint32_t* c = arrival_counter(args.counters, b * Hkv + hk);
-      const uint32_t ns = (uint32_t)(plan.split_begin[b + 1] - plan.split_begin[b]);
+      const uint32_t ns = (uint32_t)sq.ns;
       const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = prev + 1 == ns;
       if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -25,6 +25,29 @@ __device__ __forceinline__ void find_seq(const DecodePlan& plan, int x, int& b) 
     if (x >= plan.split_begin[i]) b = i;
 }
 
+// The sequence of global split x: its index, first split, split count and length (rows). A
+// single sequence (decode or verify of one stream) takes them from fixed argument offsets, in
+// one batch of argument loads with nseq; a batch searches the plan, whose index-dependent
+// argument loads are a second round trip before the kernel's first copy.
+struct SeqSplits {
+  int b, s0, ns, len;
+};
+// Kernel arguments the prologue needs before its first copy, listed as SGPR inputs of one empty
+// asm statement right after they are read: the compiler then issues all their loads in one batch
+// (left alone, it issued some only behind the first branch on the others -- a second argument
+// round trip of ~0.3 us before any copy could start).
+#define LQ_ARG_BATCH(...) asm volatile("" ::__VA_ARGS__)
+__device__ __forceinline__ SeqSplits seq_splits(const DecodePlan& plan, int x) {
+  SeqSplits s{0, 0, plan.split_begin[1], plan.len[0]};  // split_begin[0] is 0
+  if (plan.nseq > 1) {
+    find_seq(plan, x, s.b);
+    s.s0 = plan.split_begin[s.b];
+    s.ns = plan.split_begin[s.b + 1] - s.s0;
+    s.len = plan.len[s.b];
+  }
+  return s;
+}
+
 // Arguments of the attention kernels (kernel argument block, passed by value).
 struct AttnArgs {
   const uint16_t* q;  // bf16 [B, Hkv * G, L, D]

@@ -84,23 +84,27 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   const int Hkv = args.Hkv, G = args.G, L = args.L;
   const int64_t cap = args.cap;
   const float qk_scale_log2 = args.qk_scale_log2;
+  LQ_ARG_BATCH("s"(q), "s"(kc), "s"(ks), "s"(kb), "s"(vc), "s"(vs), "s"(vb), "s"(args.knew),
+               "s"(args.vnew), "s"(args.pos), "s"(args.counters), "s"(cap), "s"(Hkv), "s"(G),
+               "s"(L), "s"(nargs.qn_w), "s"(nargs.kn_w), "s"(nargs.inv_freq), "s"(plan.nseq),
+               "s"(plan.split_begin[1]), "s"(plan.len[0]));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
   const int x = blockIdx.x;
   const int hk = blockIdx.y;
-  int b;
-  find_seq(plan, x, b);
-  const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap) : plan.len[b];
+  const SeqSplits sq = seq_splits(plan, x);
+  const int b = sq.b;
+  const int n = args.pos ? (int)min(max((int64_t)args.pos[b] + 1, (int64_t)1), args.cap) : sq.len;
   // Work in super-tiles of PST keys. The NWS waves of the sequence's workgroups take about 90%
   // of them statically (wave gw: super-tiles gw + k NWS for k < NS), the rest one at a time from
   // the (sequence, KV head) tile counter, two super-tiles ahead. Waves that started late or sit
   // on busier parts of the chip (XCDs start up to ~3 us apart and differ by ~10% in the
   // bandwidth they get) then take fewer of the dynamic super-tiles.
   const int T = (n + PST - 1) / PST;
-  const int NWS = (plan.split_begin[b + 1] - plan.split_begin[b]) * NWAVE;
-  const int gw = (x - plan.split_begin[b]) * NWAVE + wv;
+  const int NWS = sq.ns * NWAVE;
+  const int gw = (x - sq.s0) * NWAVE + wv;
   const int NS = max(2, (9 * T) / (10 * NWS));  // static super-tiles per wave
   const int R = G * L;  // <= 4
   // Fused append: the wave that gets super-tile app_t (holding row n - 1, the sequence's new last
