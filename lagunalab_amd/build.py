@@ -36,12 +36,18 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags. layer.hip: the decode-step kernels take plain pointer and scalar
+# arguments, and gfx950's dispatch preloads the leading ones (up to 14 dwords: a GEMV's five
+# pointers and N, K, eps) into SGPRs, so their first loads wait for no argument round trip.
+EXTRA_FLAGS = {"layer.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(hipcc, src, obj):
-    cmd = [hipcc, *FLAGS, "-c", "-o", str(obj), str(src)]
+    cmd = [hipcc, *FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", "-o", str(obj), str(src)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     return cmd, r
 
