@@ -40,6 +40,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
                                                            DecodePlan plan,
                                                            uint16_t* __restrict__ out) {
   constexpr int PER = MS / 4;
+  // one batch of argument loads: a single sequence's split range sits at fixed offsets (an
+  // index-dependent load would be a second argument round trip before the first partial load)
+  LQ_ARG_BATCH("s"(part_acc), "s"(part_ml), "s"(rows), "s"(total_rows), "s"(plan.nseq),
+               "s"(plan.split_begin[1]));
   const int grow = blockIdx.x >> 1;  // (sequence, row) index
   if (grow >= total_rows) return;    // workgroup-uniform
   const int lane = threadIdx.x;
@@ -47,8 +51,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
   const int d0 = 64 * (blockIdx.x & 1) + 4 * (lane & 15);
   const int b = grow / rows;
   const int hq = grow - b * rows;
-  const int s0 = plan.split_begin[b];
-  const int ns = min(plan.split_begin[b + 1] - s0, MS);
+  int s0 = 0, ns = min(plan.split_begin[1], MS);
+  if (plan.nseq > 1) {
+    s0 = plan.split_begin[b];
+    ns = min(plan.split_begin[b + 1] - s0, MS);
+  }
   float m[PER], l[PER];
   float4 a[PER];
   // The (m, l) index is the same in 16 lanes; hidden from the compiler so that the loads stay
