@@ -272,10 +272,14 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 // out [B, Hq, L, D] (bf16). Partial (m, l, acc) of split s, row r: part_ml / part_acc at
 // (s * Hkv + hk) * R + r.
 // Thread t takes 4 dims (t % 32) of row (t % 32 RW) / 32 over the splits of parity t / 32 RW (one
-// to four parities: NW * 64 / (32 RW)): it loads (m, l, acc) of up to MCH splits at once (one
-// memory round trip for up to MCH splits per parity: 16 with one or two parities, 8 with four),
-// merges them with its own running max, and the parities meet in LDS. red: LDS scratch of at
-// least 6 * 32 RW * max(1, parities - 1) floats.
+// to four parities: NW * 64 / (32 RW)): it loads the acc of up to MCH splits at once (one memory
+// round trip for up to MCH splits per parity: 16 with one or two parities, 8 with four), merges
+// them with its own running max, and the parities meet in LDS. The (m, l) of each (split, row)
+// are loaded once, by one thread, and shared through LDS: the 32 threads of a row all need them,
+// and as one load per thread they cost the texture path half as many bytes again as the acc
+// partials (its bytes per lane, not the unique bytes, set the merge's load time). The merging
+// kernels have at most 32 splits per sequence (the plan caps them), so one load per thread
+// covers them. red: LDS scratch of at least 6 * 32 RW * max(1, parities - 1) + 2 * 32 RW floats.
 template <int NW, int RW = 4>
 __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& plan,
                             const float* __restrict__ part_acc,
@@ -285,6 +289,7 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
   constexpr int NPAR = 64 * NW / TPR;  // split parities
   static_assert(RW == 4 || RW == 8, "4 or 8 rows per parity");
   static_assert(NPAR == 1 || NPAR == 2 || NPAR == 4, "one, two or four split parities");
+  static_assert(32 * RW <= 64 * NW, "one (m, l) load per thread covers 32 splits");
   constexpr int MCH = NPAR == 4 ? 8 : 16;
   const int tid = threadIdx.x;
   const int s0 = plan.split_begin[b];
@@ -295,56 +300,67 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
   const int row = o >> 5;
   const int d0 = 4 * (o & 31);
   const int par = tid / TPR;
+  const int rowc = min(row, R - 1);  // threads past the rows load and weigh row R - 1, unused
+  float2* const mls = reinterpret_cast<float2*>(red + 6 * TPR * (NPAR > 2 ? NPAR - 1 : 1));
+  // (m, l) of (split mi / R, row mi % R) first, then the first batch of this thread's acc
+  // partials (through one buffer resource with the sequence's first split as its wave-uniform
+  // base, 16 bytes at a 32-bit byte offset per split), all in flight before the LDS exchange
+  const int nml = ns * R;
+  const int mi = min(tid, nml - 1);
+  const int msp = mi / R;
+  const float2 mlt = ld_agent2(reinterpret_cast<const float*>(
+      part_ml + (int64_t)(s0 + msp) * rs + r0 + (mi - msp * R)));
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(part_acc + (int64_t)s0 * rs * D), 0, 0x7fffffff, 0x00020000);
+  const uint32_t abase = (uint32_t)(((r0 + rowc) * D + d0) * 4);
+  const int step = (int)rs;
+  auto load_acc = [&](int base, f4_t (&av)[MCH]) {
+#pragma unroll
+    for (int k = 0; k < MCH; ++k)
+      av[k] = ld_agent4(rsrc, abase + (uint32_t)(min(base + NPAR * k, ns - 1) * step) * (D * 4));
+  };
+  f4_t av0[MCH];
+  load_acc(par, av0);
+  if (tid < nml) mls[tid] = mlt;
+  __syncthreads();
   float M = -INFINITY, den = 0.0f;
   float a[4] = {0.f, 0.f, 0.f, 0.f};
-  if (row < R) {
-    // this thread's partials of split s0 (64-bit base once), later splits at 32-bit offsets
-    // (so the loads go out back to back, with no 64-bit multiply per split in front of them)
-    const int64_t pr0 = (int64_t)s0 * rs + r0 + row;
-    const float2* __restrict__ mlp = part_ml + pr0;
-    // the acc partials of the sequence's splits through one buffer resource (wave-uniform base:
-    // the sequence's first split), this thread's 16 bytes at a 32-bit byte offset
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(part_acc + (int64_t)s0 * rs * D), 0, 0x7fffffff, 0x00020000);
-    const uint32_t abase = (uint32_t)(((r0 + row) * D + d0) * 4);
-    const int step = (int)rs;
-    for (int base = par; base < ns; base += NPAR * MCH) {
-      float mv[MCH], lv[MCH], av[MCH][4];
+  // Branch-free: every loaded value is used on every path (with the weighting under a branch on
+  // the maxima the compiler had waited for the m values before issuing the acc loads: a second
+  // memory round trip). Splits whose rows saw no key (m = -inf) weigh 0.
+  auto weigh = [&](int base, const f4_t (&av)[MCH]) {
+    float mv[MCH], lv[MCH];
 #pragma unroll
-      for (int k = 0; k < MCH; ++k) {
-        const int off = min(base + NPAR * k, ns - 1) * step;
-        const float2 ml = ld_agent2(reinterpret_cast<const float*>(mlp + off));
-        const f4_t a4 = ld_agent4(rsrc, abase + (uint32_t)off * (D * 4));
-        mv[k] = ml.x;
-        lv[k] = ml.y;
-        av[k][0] = a4[0];
-        av[k][1] = a4[1];
-        av[k][2] = a4[2];
-        av[k][3] = a4[3];
-      }
-      // Branch-free: every loaded value is used on every path, so that the compiler issues
-      // all loads of the batch before the first wait (with the weighting under a branch on the
-      // maxima it waited for the m values, then issued the acc and l loads: a second memory
-      // round trip). Splits whose rows saw no key (m = -inf) weigh 0.
-      float cm = -INFINITY;
-#pragma unroll
-      for (int k = 0; k < MCH; ++k) cm = fmaxf(cm, base + NPAR * k < ns ? mv[k] : -INFINITY);
-      const float Mn = fmaxf(M, cm);
-      const float Mr = Mn == -INFINITY ? 0.0f : Mn;
-      const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mr);
-      den *= sc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a[j] *= sc;
-#pragma unroll
-      for (int k = 0; k < MCH; ++k) {
-        const bool use = base + NPAR * k < ns && mv[k] != -INFINITY;
-        const float w = use ? exp2_nonpos(mv[k] - Mr) : 0.0f;
-        den = fmaf(w, lv[k], den);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = fmaf(w, av[k][j], a[j]);
-      }
-      M = Mn;
+    for (int k = 0; k < MCH; ++k) {
+      const float2 ml = mls[min(base + NPAR * k, ns - 1) * R + rowc];
+      mv[k] = ml.x;
+      lv[k] = ml.y;
     }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < MCH; ++k) cm = fmaxf(cm, base + NPAR * k < ns ? mv[k] : -INFINITY);
+    const float Mn = fmaxf(M, cm);
+    const float Mr = Mn == -INFINITY ? 0.0f : Mn;
+    const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mr);
+    den *= sc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] *= sc;
+#pragma unroll
+    for (int k = 0; k < MCH; ++k) {
+      const bool use = base + NPAR * k < ns && mv[k] != -INFINITY;
+      const float w = use ? exp2_nonpos(mv[k] - Mr) : 0.0f;
+      den = fmaf(w, lv[k], den);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = fmaf(w, av[k][j], a[j]);
+    }
+    M = Mn;
+  };
+  weigh(par, av0);
+  // a parity's later batches (one parity over more than MCH splits: the bf16 kernel's two waves)
+  for (int base = par + NPAR * MCH; base < ns; base += NPAR * MCH) {
+    f4_t av[MCH];
+    load_acc(base, av);
+    weigh(base, av);
   }
   if constexpr (NPAR == 4) {
     // parities 1-3 hand (M, den, a) to parity 0 through LDS; one log-sum-exp over the four
@@ -420,7 +436,7 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
 // side, then [4][NW]: the output factors. Each output pair of dims then takes NW 8-byte reads and
 // three NW-wide reads. Then the arrival count, and the last workgroup of the (sequence, KV head)
 // merges all splits (merge_rows4, with acc_lds as its scratch). acc_lds and st_lds 16-byte
-// aligned; each wave's area at least 4 FIN_ROW floats, wave 0's at least 6 * 128 (merge
+// aligned; each wave's area at least 4 FIN_ROW floats, wave 0's at least 6 * 128 + 256 (merge
 // scratch), st_lds 20 NW floats.
 // EVEN_ODD: accumulator tile 2j + p holds dims 32 j + 2 (4 lane group + r) + p (the 4-bit
 // kernel's P.V operands); otherwise tile j holds dims 16 j + 4 lane group + r. osc: output factor

@@ -53,7 +53,7 @@ struct Q4Smem {
     int last;
   } fin;
 };
-static_assert(sizeof(Q4Buf) * 2 >= sizeof(float) * 6 * 128, "wave buffers hold the finish rows");
+static_assert(sizeof(Q4Buf) * 2 >= sizeof(float) * (6 * 128 + 256), "wave buffers hold the finish rows");
 
 // 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals, in the
 // k-slot order {0, 4, 1, 5, 2, 6, 3, 7}: masks keep two nibbles per word, one in each half, so

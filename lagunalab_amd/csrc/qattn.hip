@@ -58,7 +58,7 @@ struct PackSmem {
   } loop;
   alignas(16) float st[NWAVE][4][6];
 };
-static_assert(sizeof(PackBuf) * 2 >= sizeof(float) * 6 * 128, "wave buffers hold the finish rows");
+static_assert(sizeof(PackBuf) * 2 >= sizeof(float) * (6 * 128 + 256), "wave buffers hold the finish rows");
 
 // The NORM variant's extra staging (RoPE frequencies of each wave's copy).
 template <bool NORM>
