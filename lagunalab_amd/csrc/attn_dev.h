@@ -537,33 +537,20 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
-    float a0 = 0.0f, a1 = 0.0f;
+    // the items of a row fill one wave, whose first lane also stores the row's (M, l)
+    const wvec l = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 1) * NW);
+    float a0 = 0.0f, a1 = 0.0f, lt = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float mw = WaveVec<NW>::get(m, w);
       const float e = mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M);
       a0 += e * fmaf(ac[w].x, WaveVec<NW>::get(os0, w), WaveVec<NW>::get(bs, w));
       a1 += e * fmaf(ac[w].y, WaveVec<NW>::get(os1, w), WaveVec<NW>::get(bs, w));
+      lt += mw == -INFINITY ? 0.0f : e * WaveVec<NW>::get(l, w);
     }
-    st_agent2(args.part_acc + ((int64_t)x * Hkv * R + (int64_t)hk * R + col) * D + d, a0, a1);
-  }
-  if (tid < R) {
-    const int col = tid;
-    const wvec m = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 0) * NW);
-    const wvec l = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 1) * NW);
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
-    float lt = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float mw = WaveVec<NW>::get(m, w);
-      lt += mw == -INFINITY ? 0.0f : exp2_nonpos(mw - M) * WaveVec<NW>::get(l, w);
-    }
-    float* pml =
-        reinterpret_cast<float*>(args.part_ml + (int64_t)x * Hkv * R + (int64_t)hk * R + col);
-    st_agent(pml, M);
-    st_agent(pml + 1, lt);
+    const int64_t prow = (int64_t)x * Hkv * R + (int64_t)hk * R + col;
+    st_agent2(args.part_acc + prow * D + d, a0, a1);
+    if (d == 0) st_agent2(reinterpret_cast<float*>(args.part_ml + prow), M, lt);
   }
 
   // ---- split merge, fused: the last workgroup of (sequence, KV head) to store its partials
