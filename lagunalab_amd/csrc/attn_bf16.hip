@@ -171,8 +171,8 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
       sc[r] = v;
       tmax = fmaxf(tmax, v);
     }
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR4>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR8>(tmax));
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;

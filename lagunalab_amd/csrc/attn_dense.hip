@@ -666,7 +666,7 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
 #pragma unroll
       for (int w = 0; w < DW; ++w) {
         stw[w] = *reinterpret_cast<const float4*>(sm.st[w][col]);
-        M = fmaxf(M, stw[w].x);
+        M = max_ieee(M, stw[w].x);
       }
       float ew[DW], bias = 0.0f;
 #pragma unroll
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
       const int col = tid;
       float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < DW; ++w) M = fmaxf(M, sm.st[w][col][0]);
+      for (int w = 0; w < DW; ++w) M = max_ieee(M, sm.st[w][col][0]);
       float l = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
       for (int w = 0; w < DW; ++w) {

@@ -76,10 +76,10 @@ __device__ __forceinline__ int pow2_exp_into(float amax, int e, int lo, int hi) 
 
 // Max over all 64 lanes on the VALU (DPP row steps, then row and half swaps); all lanes active.
 __device__ __forceinline__ float wave_max_valu(float x) {
-  x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
-  x = fmaxf(x, dpp<DPP_QUAD_XOR2>(x));
-  x = fmaxf(x, dpp<DPP_ROW_ROR4>(x));
-  x = fmaxf(x, dpp<DPP_ROW_ROR8>(x));
+  x = max_ieee(x, dpp<DPP_QUAD_XOR1>(x));
+  x = max_ieee(x, dpp<DPP_QUAD_XOR2>(x));
+  x = max_ieee(x, dpp<DPP_ROW_ROR4>(x));
+  x = max_ieee(x, dpp<DPP_ROW_ROR8>(x));
   return max_xor32(max_xor16(x));
 }
 
@@ -338,8 +338,8 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
     }
     float cm = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < MCH; ++k) cm = fmaxf(cm, base + NPAR * k < ns ? mv[k] : -INFINITY);
-    const float Mn = fmaxf(M, cm);
+    for (int k = 0; k < MCH; ++k) cm = max_ieee(cm, base + NPAR * k < ns ? mv[k] : -INFINITY);
+    const float Mn = max_ieee(M, cm);
     const float Mr = Mn == -INFINITY ? 0.0f : Mn;
     const float sc = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mr);
     den *= sc;
@@ -373,7 +373,7 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
     __syncthreads();
     if (par == 0 && row < R) {
       float Mp[4] = {M, red[o], red[6 * TPR + o], red[12 * TPR + o]};
-      const float Mx = fmaxf(fmaxf(Mp[0], Mp[1]), fmaxf(Mp[2], Mp[3]));
+      const float Mx = max_ieee(max_ieee(Mp[0], Mp[1]), max_ieee(Mp[2], Mp[3]));
       float num[4] = {0.f, 0.f, 0.f, 0.f}, dsum = 0.0f;
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
@@ -411,7 +411,7 @@ __device__ void merge_rows4(int b, int hk, int Hkv, int R, const DecodePlan& pla
     }
   }
   if (par == 0 && row < R) {
-    const float Mx = fmaxf(M, M1);
+    const float Mx = max_ieee(M, M1);
     const float e0 = M == -INFINITY ? 0.0f : exp2_nonpos(M - Mx);
     const float e1 = M1 == -INFINITY ? 0.0f : exp2_nonpos(M1 - Mx);
     const float inv = 1.0f / (e0 * den + e1 * den1);
@@ -536,7 +536,7 @@ __device__ void packed_finish(f4_t (&oacc)[8], float m_run, float lsum, float bs
       ac[w] = *reinterpret_cast<const float2*>(acc_lds + w * acc_ws + col * FIN_ROW + d);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, WaveVec<NW>::get(m, w));
+    for (int w = 0; w < NW; ++w) M = max_ieee(M, WaveVec<NW>::get(m, w));
     // the items of a row fill one wave, whose first lane also stores the row's (M, l)
     const wvec l = *reinterpret_cast<const wvec*>(st_lds + (col * 4 + 1) * NW);
     float a0 = 0.0f, a1 = 0.0f, lt = 0.0f;

@@ -246,8 +246,8 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
       }
     }
     float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR4>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR8>(tmax));
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;

@@ -139,16 +139,23 @@ __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
+// IEEE 754-2019 maximum (NaN if either operand is NaN; equal to fmaxf on everything else): one
+// v_maximum3_f32. fmaxf of a value the compiler cannot prove canonical -- the result of a DPP move
+// or a lane swap -- costs a canonicalizing v_max_f32 per such operand first, three or four
+// instructions per reduction step instead of one; the attention reductions (scores, the
+// merges' maxima, |q| and |scale_v|) use this one. The quantizers keep fmaxf.
+__device__ __forceinline__ float max_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Max / sum with the lane 16 (32) apart, on the VALU: v_permlane16_swap (v_permlane32_swap)
 // exchanges whole rows of 16 (halves of 32) lanes between two registers, so combining the two
 // results gives every lane the op over itself and its partner. All 64 lanes must be active.
 __device__ __forceinline__ float max_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const float* __restric
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) M = fmaxf(M, qt + 4 * k < ns ? m[k] : -INFINITY);
+  for (int k = 0; k < PER; ++k) M = max_ieee(M, qt + 4 * k < ns ? m[k] : -INFINITY);
   M = max_xor32(max_xor16(M));
   float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f, den = 0.0f;
 #pragma unroll

@@ -278,8 +278,8 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
       tmax = fmaxf(tmax, v);
     }
     // max over the 4 key tiles (lanes 4 apart in a row) and the 4 lane groups
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR4>(tmax));
-    tmax = fmaxf(tmax, dpp<DPP_ROW_ROR8>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR4>(tmax));
+    tmax = max_ieee(tmax, dpp<DPP_ROW_ROR8>(tmax));
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     const bool bump = tmax > m_run + RESCALE_LOG2;
