@@ -204,6 +204,35 @@ __device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1 nt"
                :: "v"(voff), "s"(sbase), "s"(lds + LOFF) : "memory");
 }
+// Copy groups of a full super-tile under one M0: four 16-byte copies from rows RS bytes apart in
+// global memory to LDS destinations RS bytes apart (the immediate offset moves both), or the four
+// word arrays of a super-tile (bases pre-shifted by -OFS_j so that offset OFS_j lands each in its
+// LDS array, the arrays OFS bytes apart). One M0 write and its wait state per group instead of
+// per copy.
+template <int LOFF, int RS>
+__device__ __forceinline__ void dma4_b128(const void* sbase, uint32_t voff, uint32_t lds) {
+  static_assert(3 * RS < 4096, "immediate offsets are 12-bit");
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %0, %1 nt\n\t"
+               "global_load_lds_dwordx4 %0, %1 offset:%3 nt\n\t"
+               "global_load_lds_dwordx4 %0, %1 offset:%4 nt\n\t"
+               "global_load_lds_dwordx4 %0, %1 offset:%5 nt"
+               :: "v"(voff), "s"(sbase), "s"(lds + LOFF), "i"(RS), "i"(2 * RS), "i"(3 * RS)
+               : "memory");
+}
+template <int LOFF, int OFS>
+__device__ __forceinline__ void dma4_b32(const void* s0, const void* s1, const void* s2,
+                                         const void* s3, uint32_t voff, uint32_t lds) {
+  static_assert(3 * OFS < 4096, "immediate offsets are 12-bit");
+  asm volatile("s_mov_b32 m0, %5\n\ts_nop 0\n\t"
+               "global_load_lds_dword %0, %1 nt\n\t"
+               "global_load_lds_dword %0, %2 offset:%6 nt\n\t"
+               "global_load_lds_dword %0, %3 offset:%7 nt\n\t"
+               "global_load_lds_dword %0, %4 offset:%8 nt"
+               :: "v"(voff), "s"(s0), "s"(s1), "s"(s2), "s"(s3), "s"(lds + LOFF), "i"(OFS),
+                  "i"(2 * OFS), "i"(3 * OFS)
+               : "memory");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

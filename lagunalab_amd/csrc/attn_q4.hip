@@ -130,8 +130,19 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
 
   // 12 copies per super-tile: copy u of lane l moves 16 bytes of row 16 u + l / 4, chunk
   // (l % 4) ^ (l / 16) (= chunk position l % 4 with the row's swizzle), plus the 4 word arrays.
+  // A full super-tile takes three copy groups (K, V, words) under one M0 each, at a 32-bit
+  // per-lane offset from fixed bases (the word bases shifted back by the arrays' LDS spacing);
+  // the wave's last, partial super-tile clamps each lane's rows and goes copy by copy.
   const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
   const uint32_t col_off = (uint32_t)(16 * ((lane & 3) ^ (lane >> 4)));
+  const uint32_t ro0 = (uint32_t)((lane >> 2) * QROW) + col_off;
+  constexpr int WSP = QPST * 4;  // bytes between the word arrays in LDS
+  static_assert(offsetof(Q4Buf, kb) == offsetof(Q4Buf, ks) + WSP &&
+                offsetof(Q4Buf, vs) == offsetof(Q4Buf, ks) + 2 * WSP &&
+                offsetof(Q4Buf, vb) == offsetof(Q4Buf, ks) + 3 * WSP, "word arrays WSP apart");
+  const uint8_t* kbw_s = reinterpret_cast<const uint8_t*>(kbw) - WSP;
+  const uint8_t* vsw_s = reinterpret_cast<const uint8_t*>(vsw) - 2 * WSP;
+  const uint8_t* vbw_s = reinterpret_cast<const uint8_t*>(vbw) - 3 * WSP;
   auto issue = [&](int si, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr int OK = offsetof(Q4Buf, k), OV = offsetof(Q4Buf, v);
@@ -139,39 +150,31 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
     constexpr int OVS = offsetof(Q4Buf, vs), OVB = offsetof(Q4Buf, vb);
     const int t0 = w_begin + si * QPST;
     const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(Q4Buf));
-    const uint8_t* kb0 = kbase;
-    const uint8_t* vb0 = vbase;
-    const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
-    uint32_t ro[4], wo;
     if (t0 + QPST <= w_end) {
-      kb0 += (int64_t)t0 * QROW;
-      vb0 += (int64_t)t0 * QROW;
-      w0 += t0;
-      w1 += t0;
-      w2 += t0;
-      w3 += t0;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) ro[u] = (uint32_t)((16 * u + (lane >> 2)) * QROW) + col_off;
-      wo = 4u * (uint32_t)lane;
-    } else {
-      const int last = max(w_end - 1, 0);
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        ro[u] = (uint32_t)min(t0 + 16 * u + (lane >> 2), last) * QROW + col_off;
-      wo = 4u * (uint32_t)min(t0 + lane, last);
+      const uint32_t vo = ro0 + (uint32_t)t0 * QROW;
+      dma4_b128<OK, 16 * QROW>(kbase, vo, lb);
+      dma4_b128<OV, 16 * QROW>(vbase, vo, lb);
+      dma4_b32<OKS, WSP>(ksw, kbw_s, vsw_s, vbw_s, 4u * (uint32_t)(t0 + lane), lb);
+      return;
     }
-    dma_b128<OK + 0>(kb0, ro[0], lb);
-    dma_b128<OV + 0>(vb0, ro[0], lb);
-    dma_b128<OK + 1024>(kb0, ro[1], lb);
-    dma_b128<OV + 1024>(vb0, ro[1], lb);
-    dma_b128<OK + 2048>(kb0, ro[2], lb);
-    dma_b128<OV + 2048>(vb0, ro[2], lb);
-    dma_b128<OK + 3072>(kb0, ro[3], lb);
-    dma_b128<OV + 3072>(vb0, ro[3], lb);
-    dma_b32<OKS>(w0, wo, lb);
-    dma_b32<OKB>(w1, wo, lb);
-    dma_b32<OVS>(w2, wo, lb);
-    dma_b32<OVB>(w3, wo, lb);
+    const int last = max(w_end - 1, 0);
+    uint32_t ro[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      ro[u] = (uint32_t)min(t0 + 16 * u + (lane >> 2), last) * QROW + col_off;
+    const uint32_t wo = 4u * (uint32_t)min(t0 + lane, last);
+    dma_b128<OK + 0>(kbase, ro[0], lb);
+    dma_b128<OK + 1024>(kbase, ro[1], lb);
+    dma_b128<OK + 2048>(kbase, ro[2], lb);
+    dma_b128<OK + 3072>(kbase, ro[3], lb);
+    dma_b128<OV + 0>(vbase, ro[0], lb);
+    dma_b128<OV + 1024>(vbase, ro[1], lb);
+    dma_b128<OV + 2048>(vbase, ro[2], lb);
+    dma_b128<OV + 3072>(vbase, ro[3], lb);
+    dma_b32<OKS>(ksw, wo, lb);
+    dma_b32<OKB>(kbw, wo, lb);
+    dma_b32<OVS>(vsw, wo, lb);
+    dma_b32<OVB>(vbw, wo, lb);
   };
 
   const uint32_t sel_lo0 = mt == 0 ? ~0u : 0u, sel_hi0 = mt == 1 ? ~0u : 0u;
