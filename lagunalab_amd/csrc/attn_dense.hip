@@ -208,18 +208,24 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
 
   // NCOPY copies per super-tile: ST / 8 K + ST / 8 V (1 KB each) + the word arrays. Copy u of lane
   // l moves 16 bytes of row 8 u + l / 8, chunk l % 8 to chunk position (l % 8) ^ (l / 8) of the
-  // LDS row. A full super-tile uses the scalar row base t0 and per-lane offsets that never change;
-  // the last one clamps rows to the sequence's last row, and so do super-tiles past the end (their
-  // copies land in a buffer that is never read). With ST = 32 the word arrays go two per copy:
-  // lanes 0-31 read K scale (V scale) words, lanes 32-63 K bias (V bias) words, into the adjacent
-  // ks/kb (vs/vb) arrays of the buffer.
+  // LDS row. A full super-tile issues its K and V rows in groups of four under one M0 each (the
+  // rows 8 apart as immediate offsets, which move the LDS destination with them) at a 32-bit
+  // per-lane offset from fixed bases; the last one clamps rows to the sequence's last row and
+  // goes copy by copy, and so do super-tiles past the end (their copies land in a buffer that is
+  // never read). With ST = 32 the word arrays go two per copy: lanes 0-31 read K scale (V scale)
+  // words, lanes 32-63 K bias (V bias) words, into the adjacent ks/kb (vs/vb) arrays of the
+  // buffer; with ST = 64 the four arrays go as one group (bases shifted back by their spacing).
   const uint32_t lds_bufs = lds_addr(&sm.loop.buf[wv][0]);
   const uint32_t col_off = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
-  uint32_t row_off[ST / 8];
-#pragma unroll
-  for (int u = 0; u < ST / 8; ++u) row_off[u] = (uint32_t)(((lane >> 3) + 8 * u) * D) + col_off;
+  const uint32_t ro0 = (uint32_t)((lane >> 3) * D) + col_off;
   const uint32_t* wsel0 = lane < 32 ? ksw : kbw;  // ST = 32: this lane's word arrays
   const uint32_t* wsel1 = lane < 32 ? vsw : vbw;
+  constexpr int WSP = ST * 4;  // bytes between the word arrays in LDS
+  const uint8_t* kbase4 = kbase + 32 * D;  // ST = 64: rows 32-63 of a super-tile
+  const uint8_t* vbase4 = vbase + 32 * D;
+  const uint8_t* kbw_s = reinterpret_cast<const uint8_t*>(kbw) - WSP;
+  const uint8_t* vsw_s = reinterpret_cast<const uint8_t*>(vsw) - 2 * WSP;
+  const uint8_t* vbw_s = reinterpret_cast<const uint8_t*>(vbw) - 3 * WSP;
   auto issue = [&](int tile, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * DST;
@@ -227,52 +233,51 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
     constexpr int OK = offsetof(DenseBuf, k), OV = offsetof(DenseBuf, v);
     constexpr int OKS = offsetof(DenseBuf, ks), OKB = offsetof(DenseBuf, kb);
     constexpr int OVS = offsetof(DenseBuf, vs), OVB = offsetof(DenseBuf, vb);
-    const uint8_t* kb0 = kbase;
-    const uint8_t* vb0 = vbase;
-    const uint32_t *w0 = ksw, *w1 = kbw, *w2 = vsw, *w3 = vbw;
-    uint32_t ro[ST / 8], wo;
-    int wrow;  // ST = 32: word row of this lane
+    static_assert(OKB == OKS + WSP && OVS == OKS + 2 * WSP && OVB == OKS + 3 * WSP,
+                  "word arrays WSP apart");
     if (t0 + DST <= n) {
-      kb0 += (int64_t)t0 * D;
-      vb0 += (int64_t)t0 * D;
-      w0 += t0;
-      w1 += t0;
-      w2 += t0;
-      w3 += t0;
-#pragma unroll
-      for (int u = 0; u < ST / 8; ++u) ro[u] = row_off[u];
-      wo = 4u * (uint32_t)lane;
-      wrow = t0 + (lane & 31);
-    } else {
-#pragma unroll
-      for (int u = 0; u < ST / 8; ++u)
-        ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last_row) * D + col_off;
-      wo = 4u * (uint32_t)min(t0 + lane, last_row);
-      wrow = min(t0 + (lane & 31), last_row);
+      const uint32_t vo = ro0 + (uint32_t)t0 * D;
+      dma4_b128<OK, 8 * D>(kbase, vo, lb);
+      dma4_b128<OV, 8 * D>(vbase, vo, lb);
+      if constexpr (ST == 64) {
+        dma4_b128<OK + 32 * D, 8 * D>(kbase4, vo, lb);
+        dma4_b128<OV + 32 * D, 8 * D>(vbase4, vo, lb);
+        dma4_b32<OKS, WSP>(ksw, kbw_s, vsw_s, vbw_s, 4u * (uint32_t)(t0 + lane), lb);
+      } else {
+        const int wrow = t0 + (lane & 31);
+        dma_b32_v(wsel0 + wrow, lb + OKS);
+        dma_b32_v(wsel1 + wrow, lb + OVS);
+      }
+      return;
     }
-    dma_b128<OK + 0>(kb0, ro[0], lb);
-    dma_b128<OV + 0>(vb0, ro[0], lb);
-    dma_b128<OK + 1024>(kb0, ro[1], lb);
-    dma_b128<OV + 1024>(vb0, ro[1], lb);
-    dma_b128<OK + 2048>(kb0, ro[2], lb);
-    dma_b128<OV + 2048>(vb0, ro[2], lb);
-    dma_b128<OK + 3072>(kb0, ro[3], lb);
-    dma_b128<OV + 3072>(vb0, ro[3], lb);
+    uint32_t ro[ST / 8];
+#pragma unroll
+    for (int u = 0; u < ST / 8; ++u)
+      ro[u] = (uint32_t)min(t0 + (lane >> 3) + 8 * u, last_row) * D + col_off;
+    const uint32_t wo = 4u * (uint32_t)min(t0 + lane, last_row);
+    const int wrow = min(t0 + (lane & 31), last_row);
+    dma_b128<OK + 0>(kbase, ro[0], lb);
+    dma_b128<OK + 1024>(kbase, ro[1], lb);
+    dma_b128<OK + 2048>(kbase, ro[2], lb);
+    dma_b128<OK + 3072>(kbase, ro[3], lb);
+    dma_b128<OV + 0>(vbase, ro[0], lb);
+    dma_b128<OV + 1024>(vbase, ro[1], lb);
+    dma_b128<OV + 2048>(vbase, ro[2], lb);
+    dma_b128<OV + 3072>(vbase, ro[3], lb);
     if constexpr (ST == 64) {
-      dma_b128<OK + 4096>(kb0, ro[4 % (ST / 8)], lb);
-      dma_b128<OV + 4096>(vb0, ro[4 % (ST / 8)], lb);
-      dma_b128<OK + 5120>(kb0, ro[5 % (ST / 8)], lb);
-      dma_b128<OV + 5120>(vb0, ro[5 % (ST / 8)], lb);
-      dma_b128<OK + 6144>(kb0, ro[6 % (ST / 8)], lb);
-      dma_b128<OV + 6144>(vb0, ro[6 % (ST / 8)], lb);
-      dma_b128<OK + 7168>(kb0, ro[7 % (ST / 8)], lb);
-      dma_b128<OV + 7168>(vb0, ro[7 % (ST / 8)], lb);
-      dma_b32<OKS>(w0, wo, lb);
-      dma_b32<OKB>(w1, wo, lb);
-      dma_b32<OVS>(w2, wo, lb);
-      dma_b32<OVB>(w3, wo, lb);
+      dma_b128<OK + 4096>(kbase, ro[4 % (ST / 8)], lb);
+      dma_b128<OK + 5120>(kbase, ro[5 % (ST / 8)], lb);
+      dma_b128<OK + 6144>(kbase, ro[6 % (ST / 8)], lb);
+      dma_b128<OK + 7168>(kbase, ro[7 % (ST / 8)], lb);
+      dma_b128<OV + 4096>(vbase, ro[4 % (ST / 8)], lb);
+      dma_b128<OV + 5120>(vbase, ro[5 % (ST / 8)], lb);
+      dma_b128<OV + 6144>(vbase, ro[6 % (ST / 8)], lb);
+      dma_b128<OV + 7168>(vbase, ro[7 % (ST / 8)], lb);
+      dma_b32<OKS>(ksw, wo, lb);
+      dma_b32<OKB>(kbw, wo, lb);
+      dma_b32<OVS>(vsw, wo, lb);
+      dma_b32<OVB>(vbw, wo, lb);
     } else {
-      static_assert(OKB == OKS + 4 * ST && OVB == OVS + 4 * ST, "word arrays adjacent");
       dma_b32_v(wsel0 + wrow, lb + OKS);
       dma_b32_v(wsel1 + wrow, lb + OVS);
     }
