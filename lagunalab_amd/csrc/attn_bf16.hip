@@ -268,7 +268,7 @@ __global__ __launch_bounds__(BTHR) void bf16_attn_packed_kernel(AttnArgs args, D
   const float osc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   static_assert(sizeof(sm.buf[0]) >= sizeof(float) * (6 * 128 + 256), "wave buffers hold the finish rows");
   packed_finish<BW>(oacc, m_run, lsum, 0.0f, 0.0f, osc, reinterpret_cast<float*>(&sm.buf[0][0]),
-                    (int)(sizeof(sm.buf[0]) / sizeof(float)), &sm.st[0][0][0], &sh_last, args,
+                    (int)(2 * sizeof(Bf16Buf) / sizeof(float)), &sm.st[0][0][0], &sh_last, args,
                     plan, x, b, hk, R);
 }
 

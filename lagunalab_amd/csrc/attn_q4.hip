@@ -404,7 +404,7 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
   vscale_out(vsc, 16777216.0f, 0.0625f, osc);  // codes entered as 16 c)
   packed_finish<QW, true>(oacc, m_run, lsum, bsum0, bsum1, osc,
                           reinterpret_cast<float*>(&sm.loop.buf[0][0]),
-                          (int)(sizeof(sm.loop.buf[0]) / sizeof(float)), &sm.fin.st[0][0][0],
+                          (int)(2 * sizeof(Q4Buf) / sizeof(float)), &sm.fin.st[0][0][0],
                           &sm.fin.last, args, plan, x, b, hk, R);
 }
 

@@ -554,7 +554,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   vscale_out(vsc, 16777216.0f, 1.0f, osc);
   packed_finish<NWAVE>(oacc, m_run, lsum, bsum0, bsum1, osc,
                        reinterpret_cast<float*>(&sm.loop.buf[0][0]),
-                       (int)(sizeof(sm.loop.buf[0]) / sizeof(float)), &sm.st[0][0][0], &sh_last,
+                       (int)(2 * sizeof(PackBuf) / sizeof(float)), &sm.st[0][0][0], &sh_last,
                        args, plan, x, b, hk, R);
 }
 
