@@ -94,6 +94,12 @@ __device__ __forceinline__ float bf16x2_max_value(uint32_t m) {
   return fmaxf(bf16_lo(m), bf16_hi(m));
 }
 
+// Workgroup barrier over LDS data only: the wave's LDS operations complete, then s_barrier.
+// Vector memory operations in flight (copies into LDS counted by vmcnt) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The q exponent kq of a wave from the largest |q| element any lane of it holds (0 when q is 0).
 __device__ __forceinline__ int q_pow2_exp(float amax_lane) {
   const float m = wave_max_valu(amax_lane);

@@ -250,37 +250,76 @@ __device__ __forceinline__ RopeLane rope_lane(int lane, const float* __restrict_
   return r;
 }
 
-// RMSNorm of a row held two values per lane, then the rotation rl (from rope_lane).
-__device__ __forceinline__ uint32_t norm_rope_apply(uint32_t x2, uint32_t w2, int lane, float eps,
-                                                    const RopeLane& rl, int rot_dims, float mscale) {
-  const float x0 = bf16_lo(x2), x1 = bf16_hi(x2);
-  float ss = x0 * x0 + x1 * x1;  // sum over the wave: rows of 16 by DPP, then row swaps
-  ss += dpp<DPP_QUAD_XOR1>(ss);
-  ss += dpp<DPP_QUAD_XOR2>(ss);
-  ss += dpp<DPP_ROW_ROR4>(ss);
-  ss += dpp<DPP_ROW_ROR8>(ss);
-  ss = sum_xor32(sum_xor16(ss));
-  const float inv = rsqrtf(ss * (1.0f / 128) + eps);
-  // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
-  float y0 = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2)));
-  float y1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2)));
-
+// RMSNorm of N rows held two values per lane (row j: pair x2[j], norm weights w2[j]), then the
+// rotation rl (from rope_lane), in place. The rows go through each phase together (reductions,
+// then the partner exchanges under one branch on the partner distance, then the rotations), so
+// that their dependency chains interleave; each row's arithmetic is that of the one-row case.
+template <int N>
+__device__ __forceinline__ void norm_rope_rows(uint32_t (&x2)[N], const uint32_t (&w2)[N], int lane,
+                                               float eps, const RopeLane& rl, int rot_dims,
+                                               float mscale) {
+  float y0[N], y1[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float x0 = bf16_lo(x2[j]), x1 = bf16_hi(x2[j]);
+    float ss = x0 * x0 + x1 * x1;  // sum over the wave: rows of 16 by DPP, then row swaps
+    ss += dpp<DPP_QUAD_XOR1>(ss);
+    ss += dpp<DPP_QUAD_XOR2>(ss);
+    ss += dpp<DPP_ROW_ROR4>(ss);
+    ss += dpp<DPP_ROW_ROR8>(ss);
+    ss = sum_xor32(sum_xor16(ss));
+    const float inv = rsqrtf(ss * (1.0f / 128) + eps);
+    // RMSNorm output, rounded to bf16 (the reference's norm returns bf16)
+    y0[j] = bf16_to_f32(f32_to_bf16(x0 * inv * bf16_lo(w2[j])));
+    y1[j] = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_hi(w2[j])));
+  }
   const int half = rot_dims >> 1;      // rotated pairs
   const int lane_off = rot_dims >> 2;  // partner lane distance
   const int partner = rl.rot ? (2 * lane < half ? lane + lane_off : lane - lane_off) : lane;
-  const float p0 = rope_partner(y0, lane, lane_off, partner);
-  const float p1 = rope_partner(y1, lane, lane_off, partner);
-  if (rl.rot) {
-    const float a0 = y0 * mscale, a1 = y1 * mscale, b0 = p0 * mscale, b1 = p1 * mscale;
-    if (rl.first) {  // dims i < half: out = x_i cos - x_{i+half} sin
-      y0 = a0 * rl.c0 - b0 * rl.s0;
-      y1 = a1 * rl.c1 - b1 * rl.s1;
-    } else {  // this lane holds x_{i+half}; the partner holds x_i
-      y0 = b0 * rl.s0 + a0 * rl.c0;
-      y1 = b1 * rl.s1 + a1 * rl.c1;
+  float p0[N], p1[N];
+  if (lane_off == 16) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      p0[j] = rope_partner(y0[j], lane, 16, partner);
+      p1[j] = rope_partner(y1[j], lane, 16, partner);
+    }
+  } else if (lane_off == 32) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      p0[j] = rope_partner(y0[j], lane, 32, partner);
+      p1[j] = rope_partner(y1[j], lane, 32, partner);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      p0[j] = rope_partner(y0[j], lane, lane_off, partner);
+      p1[j] = rope_partner(y1[j], lane, lane_off, partner);
     }
   }
-  return (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    float r0 = y0[j], r1 = y1[j];
+    if (rl.rot) {
+      const float a0 = r0 * mscale, a1 = r1 * mscale, b0 = p0[j] * mscale, b1 = p1[j] * mscale;
+      if (rl.first) {  // dims i < half: out = x_i cos - x_{i+half} sin
+        r0 = a0 * rl.c0 - b0 * rl.s0;
+        r1 = a1 * rl.c1 - b1 * rl.s1;
+      } else {  // this lane holds x_{i+half}; the partner holds x_i
+        r0 = b0 * rl.s0 + a0 * rl.c0;
+        r1 = b1 * rl.s1 + a1 * rl.c1;
+      }
+    }
+    x2[j] = (uint32_t)f32_to_bf16(r0) | ((uint32_t)f32_to_bf16(r1) << 16);
+  }
+}
+
+// One row: returns the lane's output pair.
+__device__ __forceinline__ uint32_t norm_rope_apply(uint32_t x2, uint32_t w2, int lane, float eps,
+                                                    const RopeLane& rl, int rot_dims, float mscale) {
+  uint32_t x[1] = {x2};
+  const uint32_t w[1] = {w2};
+  norm_rope_rows<1>(x, w, lane, eps, rl, rot_dims, mscale);
+  return x[0];
 }
 
 __device__ __forceinline__ uint32_t norm_rope_lane(uint32_t x2, uint32_t w2, int lane, float eps,

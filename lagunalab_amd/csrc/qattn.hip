@@ -60,6 +60,16 @@ struct PackSmem {
 };
 static_assert(sizeof(PackBuf) * 2 >= sizeof(float) * (6 * 128 + 256), "wave buffers hold the finish rows");
 
+// The q rows as fp16 B operands, written once per workgroup (wave r converts row r), with each
+// row's half sums (times the score scale) and, in the NORM variant, its largest |element|; row
+// NWAVE is the zero row of the lanes that hold no operand.
+struct PackQ {
+  alignas(16) uint32_t h[NWAVE + 1][64];
+  float s[NWAVE][2];
+  float amax[NWAVE];
+};
+static_assert(NWAVE >= 4, "one wave per q row");
+
 // The NORM variant's extra staging (RoPE frequencies of each wave's copy).
 template <bool NORM>
 struct PackNormSmem {
@@ -73,6 +83,7 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
                                                     const NormArgs& nargs) {
   __shared__ PackSmem sm;
   __shared__ PackNormSmem<NORM> nsm;
+  __shared__ PackQ qsh;
   __shared__ int sh_last;
   const uint16_t* __restrict__ q = args.q;
   const uint8_t* __restrict__ kc = args.kc;
@@ -421,54 +432,68 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     asm volatile("s_waitcnt vmcnt(21)" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-  if constexpr (NORM) {
-    // Raw q rows and new K row -> RMSNorm + RoPE at position n - 1, in place: every wave
-    // normalizes and rotates its own staged copies (rows 0 .. R - 1 q, then the K row), with the
-    // rotation's sin and cos computed once for all rows; no wave touches another's copies.
-    uint8_t* own = reinterpret_cast<uint8_t*>(&tm);
-    const RopeLane rl = rope_lane(lane, &nsm.inv_freq[wv][0], nargs.rot_dims, (float)(n - 1));
-    const uint32_t wq = reinterpret_cast<const uint32_t*>(own + 1536)[lane];
-    const uint32_t wk = reinterpret_cast<const uint32_t*>(own + 1792)[lane];
-    for (int j = 0; j <= R; ++j) {  // wave-uniform
-      uint32_t* row = reinterpret_cast<uint32_t*>(own + (j < R ? j * 2 * D : 1024));
-      row[lane] = norm_rope_apply(row[lane], j < R ? wq : wk, lane, nargs.norm_eps, rl,
-                                  nargs.rot_dims, nargs.mscale);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the rows are read whole below
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
   // ---- B operands of Q.K^T: q[rho] dims 8 s .. 8 s + 7 when this lane group's tile is mt, times
-  // the wave's power-of-two q factor (every lane reads a whole row; lanes 4 apart hold all rows)
+  // the workgroup's power-of-two q factor 2^kq (from the largest |q| element of its R rows). Wave
+  // w converts row w (w < R) once for the workgroup into the shared fp16 rows, with the row's two
+  // half sums; after a barrier every lane reads its row whole (lanes 4 apart hold all rows), the
+  // lanes without an operand the zero row. The barriers wait for LDS only: the copies of
+  // super-tile 0 stay in flight.
+  const uint32_t* own = reinterpret_cast<const uint32_t*>(&tm);  // q rows 64 words apart
+  const int rw = min(wv, R - 1);  // waves past R - 1 redo the last row and store nothing
+  uint32_t xq;                    // this lane's pair (dims 2 lane, 2 lane + 1) of row rw
+  float amax;                     // the largest |q| element of the R rows, in every lane
+  if constexpr (NORM) {
+    // Raw q row rw and the new K row -> RMSNorm + RoPE at position n - 1: each wave normalizes
+    // and rotates its own staged copies, the two rows together so that their reductions
+    // interleave, with the rotation's sin and cos computed once for both. The K row goes back to
+    // the wave's copy for the append below; the rows' largest elements go through LDS.
+    uint32_t* ownw = reinterpret_cast<uint32_t*>(&tm);
+    const RopeLane rl = rope_lane(lane, &nsm.inv_freq[wv][0], nargs.rot_dims, (float)(n - 1));
+    uint32_t xr[2] = {own[64 * rw + lane], own[256 + lane]};  // q row rw; K row at byte 1024
+    const uint32_t wr[2] = {own[384 + lane], own[448 + lane]};  // norm weights, bytes 1536, 1792
+    norm_rope_rows<2>(xr, wr, lane, nargs.norm_eps, rl, nargs.rot_dims, nargs.mscale);
+    ownw[256 + lane] = xr[1];
+    xq = xr[0];
+    const float m = wave_max_valu(fmaxf(fabsf(bf16_lo(xq)), fabsf(bf16_hi(xq))));
+    if (lane == 0) qsh.amax[wv] = m;
+    lds_barrier();
+    amax = qsh.amax[0];
+#pragma unroll
+    for (int j = 1; j < NWAVE; ++j)
+      if (j < R) amax = fmaxf(amax, qsh.amax[j]);
+  } else {
+    xq = own[64 * rw + lane];
+    amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NWAVE; ++j)
+      if (j < R) {
+        const uint32_t w = own[64 * j + lane];
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w))));
+      }
+  }
   {
-    const bool on = qvalid && mt == lq4;
-    const uint8_t* qr = reinterpret_cast<const uint8_t*>(&tm) + (gh * L + qi) * 2 * D;
-    uint32_t w[64];
-#pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * st);
-      w[4 * st] = u.x;
-      w[4 * st + 1] = u.y;
-      w[4 * st + 2] = u.z;
-      w[4 * st + 3] = u.w;
-    }
-    uint32_t mbits = 0u;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) mbits = bf16x2_absmax_bits(mbits, w[i]);
-    const int kq = q_pow2_exp(qvalid ? bf16x2_max_value(mbits) : 0.0f);
+    const int kq = q_pow2_exp(amax);
     const float qf = pow2f(kq);
     kscale = qk_scale_log2 * pow2f(24 - kq);
-    float sg[2] = {0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const float lo = bf16_lo(w[i]), hi = bf16_hi(w[i]);
-      sg[i >> 5] += lo + hi;
-      qb[i >> 2][2 * (i & 3)] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
-      qb[i >> 2][2 * (i & 3) + 1] = on ? (_Float16)(hi * qf) : (_Float16)0.0f;
+    if (wv < R) {
+      const float lo = bf16_lo(xq), hi = bf16_hi(xq);
+      qsh.h[wv][lane] = pack_h2(lo * qf, hi * qf);
+      float sg = lo + hi;  // over dims 0-63 (lanes 0-31) and 64-127 (lanes 32-63)
+      sg += dpp<DPP_QUAD_XOR1>(sg);
+      sg += dpp<DPP_QUAD_XOR2>(sg);
+      sg += dpp<DPP_ROW_ROR4>(sg);
+      sg += dpp<DPP_ROW_ROR8>(sg);
+      sg = sum_xor16(sg);
+      if ((lane & 31) == 0) qsh.s[wv][lane >> 5] = sg * qk_scale_log2;
     }
-    qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
-    qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
+    if (wv == 0) qsh.h[NWAVE][lane] = 0u;
+    lds_barrier();
+    const bool on = qvalid && mt == lq4;
+    const half8_t* qr = reinterpret_cast<const half8_t*>(&qsh.h[on ? rho : NWAVE][0]);
+#pragma unroll
+    for (int st = 0; st < 16; ++st) qb[st] = qr[st];
+    qsum[0] = qvalid ? qsh.s[rho][0] : 0.0f;
+    qsum[1] = qvalid ? qsh.s[rho][1] : 0.0f;
   }
   // Super-tile 1 goes out only now, behind every wave's super-tile 0 (~18 MB over the chip at
   // 82,671 keys): issued together, the two landed in the same window, so the loop waited for
