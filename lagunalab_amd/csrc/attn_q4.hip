@@ -55,6 +55,15 @@ struct Q4Smem {
 };
 static_assert(sizeof(Q4Buf) * 2 >= sizeof(float) * (6 * 128 + 256), "wave buffers hold the finish rows");
 
+// The q rows as fp16 B operands in k-slot order, written once per workgroup (wave r converts row
+// r), with each row's half sums times the score scale; row QW is the zero row of the lanes that
+// hold no operand.
+struct Q4QRows {
+  alignas(16) _Float16 h[QW + 1][128];
+  float s[QW][2];
+};
+static_assert(QW >= 4, "one wave per q row");
+
 // 8 nibble codes of one word (element 2j in the low nibble of byte j) as fp16 subnormals, in the
 // k-slot order {0, 4, 1, 5, 2, 6, 3, 7}: masks keep two nibbles per word, one in each half, so
 // that each 16-bit half holds one code. Low nibbles land at c * 2^-24, high nibbles (bits 4-7 of a
@@ -71,6 +80,7 @@ __device__ __forceinline__ half8_t nib8_sub(uint32_t w) {
 template <bool CAUSAL>
 __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, DecodePlan plan) {
   __shared__ Q4Smem sm;
+  __shared__ Q4QRows qsh;
 
   const uint16_t* __restrict__ q = args.q;
   const uint8_t* __restrict__ kc = args.kc;
@@ -341,39 +351,48 @@ __global__ __launch_bounds__(QTHR) void q4_attn_packed_kernel(AttnArgs args, Dec
   else
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  {  // q operands times the wave's power-of-two q factor (every lane reads a whole row)
-    const bool on = qvalid && mt == lq4;
-    const uint8_t* qr = reinterpret_cast<const uint8_t*>(&tm) + (gh * L + qi) * 2 * D;
-    uint32_t w[64];
+  // q operands times the workgroup's power-of-two q factor 2^kq (from the largest |q| element of
+  // its R rows): wave w converts row w (w < R) once for the workgroup into the shared fp16 rows,
+  // with the row's two half sums; after a barrier over LDS (the copies of super-tile 0 stay in
+  // flight) every lane reads its row whole, the lanes without an operand the zero row. Dim 8 s + e
+  // goes to k-slot {0, 2, 4, 6, 1, 3, 5, 7}[e] of qb[s] (the order nib8_sub gives the codes), odd
+  // dims times 1/16 (their codes enter at 16 c * 2^-24).
+  {
+    const uint32_t* own = reinterpret_cast<const uint32_t*>(&tm);  // q rows 64 words apart
+    float amax = 0.0f;
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const uint4 u = *reinterpret_cast<const uint4*>(qr + 16 * st);
-      w[4 * st] = u.x;
-      w[4 * st + 1] = u.y;
-      w[4 * st + 2] = u.z;
-      w[4 * st + 3] = u.w;
-    }
-    uint32_t mbits = 0u;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) mbits = bf16x2_absmax_bits(mbits, w[i]);
-    const int kq = q_pow2_exp(qvalid ? bf16x2_max_value(mbits) : 0.0f);
+    for (int j = 0; j < QW; ++j)
+      if (j < R) {
+        const uint32_t w = own[64 * j + lane];
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w))));
+      }
+    const int kq = q_pow2_exp(amax);
     const float qf = pow2f(kq);
     kscale = qk_scale_log2 * pow2f(24 - kq);
-    // dim 8 s + e goes to k-slot {0, 2, 4, 6, 1, 3, 5, 7}[e] of qb[s] (the order nib8_sub gives
-    // the codes), odd dims times 1/16 (their codes enter at 16 c * 2^-24)
-    float sg[2] = {0.f, 0.f};
-    const float qf16 = qf * 0.0625f;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const float lo = bf16_lo(w[i]), hi = bf16_hi(w[i]);
-      sg[i >> 5] += lo + hi;
-      const int e = 2 * (i & 3);               // dims 8 s + e and 8 s + e + 1
+    if (wv < R) {  // lane l: dims 2 l, 2 l + 1 = dims e, e + 1 of slab s = l / 4, e = 2 (l % 4)
+      const uint32_t xq = own[64 * wv + lane];
+      const float lo = bf16_lo(xq), hi = bf16_hi(xq);
+      const int e = 2 * (lane & 3);
       const int slot = 2 * (e & 2) + (e >> 2);  // k-slot of dim e; dim e + 1 sits two slots on
-      qb[i >> 2][slot] = on ? (_Float16)(lo * qf) : (_Float16)0.0f;
-      qb[i >> 2][slot + 2] = on ? (_Float16)(hi * qf16) : (_Float16)0.0f;
+      _Float16* hrow = &qsh.h[wv][8 * (lane >> 2)];
+      hrow[slot] = (_Float16)(lo * qf);
+      hrow[slot + 2] = (_Float16)(hi * (qf * 0.0625f));
+      float sg = lo + hi;  // over dims 0-63 (lanes 0-31) and 64-127 (lanes 32-63)
+      sg += dpp<DPP_QUAD_XOR1>(sg);
+      sg += dpp<DPP_QUAD_XOR2>(sg);
+      sg += dpp<DPP_ROW_ROR4>(sg);
+      sg += dpp<DPP_ROW_ROR8>(sg);
+      sg = sum_xor16(sg);
+      if ((lane & 31) == 0) qsh.s[wv][lane >> 5] = sg * qk_scale_log2;
     }
-    qsum[0] = qvalid ? sg[0] * qk_scale_log2 : 0.0f;
-    qsum[1] = qvalid ? sg[1] * qk_scale_log2 : 0.0f;
+    if (wv == 0) reinterpret_cast<uint32_t*>(&qsh.h[QW][0])[lane] = 0u;
+    lds_barrier();
+    const bool on = qvalid && mt == lq4;
+    const half8_t* qr = reinterpret_cast<const half8_t*>(&qsh.h[on ? rho : QW][0]);
+#pragma unroll
+    for (int st = 0; st < 16; ++st) qb[st] = qr[st];
+    qsum[0] = qvalid ? qsh.s[rho][0] : 0.0f;
+    qsum[1] = qvalid ? qsh.s[rho][1] : 0.0f;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // q reads done before terms overwrite
   __builtin_amdgcn_wave_barrier();
