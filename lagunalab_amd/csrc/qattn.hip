@@ -175,7 +175,9 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   const uint8_t* kbw_s = reinterpret_cast<const uint8_t*>(kbw) - WSP;
   const uint8_t* vsw_s = reinterpret_cast<const uint8_t*>(vsw) - 2 * WSP;
   const uint8_t* vbw_s = reinterpret_cast<const uint8_t*>(vbw) - 3 * WSP;
-  auto issue = [&](int tile, auto bufc) {
+  // `between(j)` runs after copy group j (0-2) of a full super-tile, after all copies otherwise:
+  // work placed there issues while the memory pipeline takes the copies issued before it.
+  auto issue_with = [&](int tile, auto bufc, auto&& between) {
     constexpr int BUF = decltype(bufc)::value;
     const int t0 = tile * PST;
     const uint32_t lb = lds_bufs + (uint32_t)(BUF * sizeof(PackBuf));
@@ -185,8 +187,11 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     if (t0 + PST <= n) {
       const uint32_t vo = ro0 + (uint32_t)t0 * D;
       dma4_b128<OK, 8 * D>(kbase, vo, lb);
+      between(0);
       dma4_b128<OV, 8 * D>(vbase, vo, lb);
+      between(1);
       dma4_b128<OK + 32 * D, 8 * D>(kbase4, vo, lb);
+      between(2);
       dma4_b128<OV + 32 * D, 8 * D>(vbase4, vo, lb);
       dma4_b32<OKS, WSP>(ksw, kbw_s, vsw_s, vbw_s, 4u * (uint32_t)(t0 + lane), lb);
       return;
@@ -216,7 +221,11 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
     dma_b32<OKB>(kbw, wo, lb);
     dma_b32<OVS>(vsw, wo, lb);
     dma_b32<OVB>(vbw, wo, lb);
+    between(0);
+    between(1);
+    between(2);
   };
+  auto issue = [&](int tile, auto bufc) { issue_with(tile, bufc, [](int) {}); };
 
   // Lane masks selecting the P.V B-operand half of K-step e (key tile 2e in slots 0-3, 2e+1 in
   // slots 4-7): this lane's own key tile is mt.
@@ -498,19 +507,32 @@ __device__ __forceinline__ void q8_attn_packed_body(const AttnArgs& args, const 
   // Super-tile 1 goes out only now, behind every wave's super-tile 0 (~18 MB over the chip at
   // 82,671 keys): issued together, the two landed in the same window, so the loop waited for
   // super-tile 0 until both were nearly in (37.6 -> 36.7 us per fused decode step).
-  if (nxt < T) issue(nxt, B1);
+  // The new K and V rows are quantized between its copy groups (the copies issue at the memory
+  // pipeline's rate, ~1.2 us for a super-tile's 20 per wave with every wave's super-tile 0 in
+  // flight, and the quantization's dependent divisions take ~1 us on their own).
   QPair app_k = {0u, 0, 0}, app_v = {0u, 0, 0};
   uint32_t app_w[4] = {0u, 0u, 0u, 0u};  // ks, kb, vs, vb words of the new row (group 0 low)
   bool patched = false;
-  if (app) {
-    const uint8_t* st8 = reinterpret_cast<const uint8_t*>(&tm);
-    app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1024 + 4 * lane));
-    app_v = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1280 + 4 * lane));
-    const uint16_t hv[4] = {app_k.scale, app_k.bias, app_v.scale, app_v.bias};
+  const uint8_t* st8 = reinterpret_cast<const uint8_t*>(&tm);
+  auto quantize_new = [&](int j) {
+    if (!app) return;
+    if (j == 0) app_k = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1024 + 4 * lane));
+    if (j == 1) app_v = quantize_pair_q8(*reinterpret_cast<const uint32_t*>(st8 + 1280 + 4 * lane));
+    if (j == 2) {
+      const uint16_t hv[4] = {app_k.scale, app_k.bias, app_v.scale, app_v.bias};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      app_w[j] = (uint32_t)__builtin_amdgcn_readlane((int)hv[j], 0) |
-                 ((uint32_t)__builtin_amdgcn_readlane((int)hv[j], 32) << 16);
+      for (int i = 0; i < 4; ++i)
+        app_w[i] = (uint32_t)__builtin_amdgcn_readlane((int)hv[i], 0) |
+                   ((uint32_t)__builtin_amdgcn_readlane((int)hv[i], 32) << 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keeps the work between the copy groups
+  };
+  if (nxt < T) {
+    issue_with(nxt, B1, quantize_new);
+  } else {
+    quantize_new(0);
+    quantize_new(1);
+    quantize_new(2);
   }
   // Overwrites row app_r of an LDS super-tile with the new row (same swizzle as the copies:
   // chunk c of row r at chunk position c ^ (r & 7); lane l holds bytes 2l, 2l+1 = chunk l / 8).
