@@ -492,8 +492,9 @@ def make_trimmable_cache(model, slack=64):
 
 def make_quantized_cache(model, bits=8, group_size=64, quantized_decode=False, fused_decode=False,
                          trim_slack=None, fused_prefill=False):
-    """Quantized KV storage on full-attention layers; sliding layers keep their window
-    (``laguna_mlx/cache.py:147-157``). Extensions: with ``trim_slack`` the sliding layers get
+    """One cache per layer: a :class:`DequantKVCache` (8- or 4-bit codes) for each full-attention
+    layer and a rotating window for each sliding-window layer, as the reference's factory lays
+    them out (``laguna_mlx/cache.py:147-157``). Extensions: with ``trim_slack`` the sliding layers get
     :class:`TrimmableWindowCache` with that slack, so that every layer can be trimmed and the
     speculative loop can run over the quantized cache; ``fused_prefill`` is passed to every
     :class:`DequantKVCache`."""

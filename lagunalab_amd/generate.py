@@ -62,7 +62,7 @@ def generate_lookup(model, prompt, max_tokens, eos=(), g=4, n_draft=7, adaptive=
     prefill_s = time.perf_counter() - t0
     token = int(torch.argmax(logits.float()))
     index = NgramIndex(g)
-    index.extend(prompt + [token])  # ids = prompt + emitted + pending token
+    index.extend(prompt + [token])  # the index covers the prompt and the first greedy token
     out, cap = [], n_draft
     stats = {"steps": 0, "drafted": 0, "accepted": 0, "steps_with_draft": 0}
     while True:
