@@ -5,9 +5,9 @@
 //
 // Same plan and structure as the packed 8-bit kernel (qattn.hip), with what 4 bits change:
 //  * A 64-key super-tile is 4 KB of K, 4 KB of V and the four scale/bias word arrays (12 copies);
-//    the whole workgroup needs 80 KB of LDS, so two could share a CU, but at long contexts the
-//    32-split cap of the in-kernel merge leaves one workgroup per CU (64 splits on two per CU
-//    were slower).
+//    with the shared q rows the workgroup takes 83.6 KB of LDS, one workgroup per CU (at long
+//    contexts the 32-split cap of the in-kernel merge gives one per CU anyway; 64 splits on two
+//    per CU, when two still fitted, were slower).
 //  * Rows are 64 bytes; chunk c of row r sits at chunk position c ^ ((r >> 2) & 3), which puts
 //    the 16 rows read together in 16 different bank quarters.
 //  * Codes become fp16 subnormals by masking: a 16-bit half keeps one nibble, at c * 2^-24 (low
