@@ -489,15 +489,24 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
         dma_b128<0>(qblk, (uint32_t)min(1024 * i + 16 * lane, qbytes - 16), qlds + 1024 * i);
   }
   // staging wave: the new rows sr0 + si + nstage i (at most 8 with L <= 16), loads issued
-  // together with q's
-  uint32_t kraw[8], vraw[8];
+  // together with q's. They are inline asm, in the staging waves only, so that the compiler
+  // inserts no wait of its own for them: its count
+  // would not include the asm copies of super-tile 0 issued after them, and its wait before the
+  // first use waited for those too, i.e. the staged rows were quantized only once super-tile 0
+  // had landed. The explicit wait below covers them (they are older than super-tile 0's copies),
+  // and the empty statement after it takes them as in-out operands, so no use moves above it.
+  uint32_t kraw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u}, vraw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  if (stager) {  // wave-uniform; a staging wave reads rows past sr1 as row sr1 - 1, unused
+    const int64_t hrow = ((int64_t)b * Hkv + hk) * L - na;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = sr0 + si + nstage * i;
-    const bool on = stager && row < sr1;
-    const int64_t src = (((int64_t)b * Hkv + hk) * L + (row - na)) * D + 2 * lane;
-    kraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.knew + src) : 0u;
-    vraw[i] = on ? *reinterpret_cast<const uint32_t*>(args.vnew + src) : 0u;
+    for (int i = 0; i < 8; ++i) {
+      const int row = min(sr0 + si + nstage * i, sr1 - 1);
+      const int64_t src = (hrow + row) * D + 2 * lane;
+      asm volatile("global_load_dword %0, %1, off"
+                   : "+v"(kraw[i]) : "v"(args.knew + src) : "memory");
+      asm volatile("global_load_dword %0, %1, off"
+                   : "+v"(vraw[i]) : "v"(args.vnew + src) : "memory");
+    }
   }
   if (cur < T) issue(cur, B0);
   if (cur < T) {  // the q copies and the new rows have landed
@@ -508,6 +517,10 @@ __global__ __launch_bounds__(64 * DW, 1) void q8_attn_dense_kernel(AttnArgs args
   } else {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  asm volatile("" : "+v"(kraw[0]), "+v"(kraw[1]), "+v"(kraw[2]), "+v"(kraw[3]), "+v"(kraw[4]),
+               "+v"(kraw[5]), "+v"(kraw[6]), "+v"(kraw[7]), "+v"(vraw[0]), "+v"(vraw[1]),
+               "+v"(vraw[2]), "+v"(vraw[3]), "+v"(vraw[4]), "+v"(vraw[5]), "+v"(vraw[6]),
+               "+v"(vraw[7]));
 
   // q operands: one power-of-two factor for all rows of the wave (the largest |q| element of any
   // row in [2^14, 2^15) before the fp16 conversion); 2^-kq goes into kscale
